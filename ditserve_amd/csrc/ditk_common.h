@@ -1,0 +1,110 @@
+// Shared helpers for the ditk HIP kernels (gfx950 / CDNA4 only).
+//
+// Conventions used by every kernel in this library:
+//   * activations and weights are bf16 stored as uint16_t, row-major, with an
+//     explicit leading dimension (elements) per tensor;
+//   * accumulation and all normalisation / modulation math is fp32;
+//   * float -> bf16 is round-to-nearest-even (NaN stays NaN);
+//   * packed batches are described by an int32 cu_seqlens table on the device;
+//     a token's segment is found by binary search, so per-token results never
+//     depend on where a segment sits in the packed buffer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DITK_EXPORT extern "C" __attribute__((visibility("default")))
+
+typedef uint16_t bf16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+
+// ---------------------------------------------------------------------------
+// error plumbing (host)
+// ---------------------------------------------------------------------------
+void ditk_set_error(const char* fmt, ...);
+int ditk_check_launch(const char* what);
+
+#define DITK_REQUIRE(cond, ...)        \
+  do {                                 \
+    if (!(cond)) {                     \
+      ditk_set_error(__VA_ARGS__);     \
+      return 1;                        \
+    }                                  \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32 (device)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// round an fp32 value to the nearest bf16 and return it as fp32
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// unpack 8 bf16 held in a 16-byte vector
+__device__ __forceinline__ void unpack8(const u32x4_t v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(v[i] << 16);
+    out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4_t pack8(const float* in) {
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf2(in[2 * i], in[2 * i + 1]);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+template <int WIDTH>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// segment of token t in cu[0..nseg] (cu[0] = 0, nondecreasing); tokens at or
+// beyond cu[nseg] map to nseg - 1.
+__device__ __forceinline__ int find_segment(const int32_t* __restrict__ cu, int nseg, int t) {
+  int lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  // 0.5 x (1 + tanh(u)) == x * sigmoid(2u),  u = sqrt(2/pi) (x + 0.044715 x^3)
+  const float k0 = 0.7978845608028654f;
+  const float k1 = 0.044715f;
+  float u = k0 * fmaf(k1 * x, x * x, x);
+  return x / (1.0f + __expf(-2.0f * u));
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }

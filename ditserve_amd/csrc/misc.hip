@@ -1,0 +1,161 @@
+// Bandwidth-bound glue of the packet prelude / epilogue and of SD3.5 joint
+// attention: patchify, unpatchify, sinusoidal timestep embedding, CFG combine,
+// joint-sequence gather / scatter.  Each is a plain coalesced elementwise pass.
+#include <math.h>
+
+#include "ditk_common.h"
+
+namespace {
+
+// latent [C, F, H, W] (bf16) -> patches [S, C*pt*ph*pw] (bf16), token order
+// f-major, then h, then w; patch vector order (c, i, j, l) as a Conv3d weight.
+__global__ void patchify_kernel(const bf16_t* __restrict__ lat, bf16_t* __restrict__ out, int C, int F,
+                                int H, int W, int pt, int ph, int pw) {
+  const int Fp = F / pt, Hp = H / ph, Wp = W / pw;
+  const int P = C * pt * ph * pw;
+  const int64_t n = (int64_t)Fp * Hp * Wp * P;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int64_t s = idx / P;
+    int p = (int)(idx % P);
+    int c = p / (pt * ph * pw), r = p % (pt * ph * pw);
+    int i = r / (ph * pw), j = (r / pw) % ph, l = r % pw;
+    int f = (int)(s / ((int64_t)Hp * Wp)), hh = (int)((s / Wp) % Hp), ww = (int)(s % Wp);
+    out[idx] = lat[(((int64_t)c * F + f * pt + i) * H + hh * ph + j) * W + ww * pw + l];
+  }
+}
+
+// x [S, pt*ph*pw*C] (bf16, feature order (i, j, l, c)) -> latent [C, F, H, W] (fp32)
+__global__ void unpatchify_kernel(const bf16_t* __restrict__ x, int64_t ldx, float* __restrict__ out,
+                                  int C, int Fp, int Hp, int Wp, int pt, int ph, int pw) {
+  const int F = Fp * pt, H = Hp * ph, W = Wp * pw;
+  const int64_t n = (int64_t)C * F * H * W;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int w = (int)(idx % W);
+    int h = (int)((idx / W) % H);
+    int f = (int)((idx / ((int64_t)W * H)) % F);
+    int c = (int)(idx / ((int64_t)W * H * F));
+    int64_t s = ((int64_t)(f / pt) * Hp + h / ph) * Wp + w / pw;
+    int feat = (((f % pt) * ph + h % ph) * pw + w % pw) * C + c;
+    out[idx] = bf2f(x[s * ldx + feat]);
+  }
+}
+
+// emb[n, :] = [cos(t_n * f_k), sin(t_n * f_k)],  f_k = exp(-ln(max_period) * k / half)
+// (flip_sin_to_cos ordering, frequency shift 0), bf16 out.
+__global__ void timestep_embed_kernel(const float* __restrict__ t, bf16_t* __restrict__ out, int N, int dim,
+                                      float log_max_period) {
+  const int half = dim / 2;
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)N * dim) return;
+  int n = (int)(idx / dim), k = (int)(idx % dim);
+  int kk = k % half;
+  float freq = expf(-log_max_period * (float)kk / (float)half);
+  float a = t[n] * freq;
+  out[idx] = f2bf(k < half ? cosf(a) : sinf(a));
+}
+
+// out = u + g * (c - u)
+__global__ void cfg_combine_kernel(const float* __restrict__ cond, const float* __restrict__ uncond,
+                                   float* __restrict__ out, int64_t n, float g) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = uncond[i] + g * (cond[i] - uncond[i]);
+}
+
+// joint[cu_joint[m] + r] = img[cu_img[m] + r] for r < n_img(m), then txt rows.
+// direction 0: gather (img, txt -> joint); 1: scatter (joint -> img, txt).
+__global__ void joint_copy_kernel(bf16_t* __restrict__ img, int64_t ld_img, bf16_t* __restrict__ txt,
+                                  int64_t ld_txt, bf16_t* __restrict__ joint, int64_t ld_joint,
+                                  const int32_t* __restrict__ cu_img, const int32_t* __restrict__ cu_txt,
+                                  int nseg, int total, int width, int direction) {
+  const int row = blockIdx.x;
+  if (row >= total) return;
+  int m = 0;
+  {
+    int lo = 0, hi = nseg - 1;
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (cu_img[mid] + cu_txt[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    m = lo;
+  }
+  const int r = row - (cu_img[m] + cu_txt[m]);
+  const int n_img = cu_img[m + 1] - cu_img[m];
+  bf16_t* src = (r < n_img) ? img + (int64_t)(cu_img[m] + r) * ld_img
+                            : txt + (int64_t)(cu_txt[m] + r - n_img) * ld_txt;
+  bf16_t* j = joint + (int64_t)row * ld_joint;
+  for (int c = threadIdx.x; c < width / 8; c += blockDim.x) {
+    if (direction == 0)
+      reinterpret_cast<u32x4_t*>(j)[c] = reinterpret_cast<const u32x4_t*>(src)[c];
+    else
+      reinterpret_cast<u32x4_t*>(src)[c] = reinterpret_cast<const u32x4_t*>(j)[c];
+  }
+}
+
+__global__ void silu_kernel(const bf16_t* __restrict__ x, bf16_t* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = f2bf(silu_f(bf2f(x[i])));
+}
+
+inline unsigned grid_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  return (unsigned)(b > 65536 ? 65536 : (b < 1 ? 1 : b));
+}
+
+}  // namespace
+
+DITK_EXPORT int ditk_patchify(const void* latent, void* out, int C, int F, int H, int W, int pt, int ph,
+                              int pw, hipStream_t stream) {
+  DITK_REQUIRE(latent && out, "ditk_patchify: null tensor");
+  DITK_REQUIRE(pt > 0 && ph > 0 && pw > 0 && F % pt == 0 && H % ph == 0 && W % pw == 0,
+               "ditk_patchify: latent %dx%dx%d not divisible by patch %dx%dx%d", F, H, W, pt, ph, pw);
+  int64_t n = (int64_t)C * F * H * W;
+  patchify_kernel<<<grid_for(n), 256, 0, stream>>>((const bf16_t*)latent, (bf16_t*)out, C, F, H, W, pt, ph, pw);
+  return ditk_check_launch("ditk_patchify");
+}
+
+DITK_EXPORT int ditk_unpatchify(const void* x, int64_t ldx, float* out, int C, int Fp, int Hp, int Wp,
+                                int pt, int ph, int pw, hipStream_t stream) {
+  DITK_REQUIRE(x && out, "ditk_unpatchify: null tensor");
+  DITK_REQUIRE(ldx >= (int64_t)C * pt * ph * pw, "ditk_unpatchify: ldx too small");
+  int64_t n = (int64_t)C * Fp * pt * Hp * ph * Wp * pw;
+  unpatchify_kernel<<<grid_for(n), 256, 0, stream>>>((const bf16_t*)x, ldx, out, C, Fp, Hp, Wp, pt, ph, pw);
+  return ditk_check_launch("ditk_unpatchify");
+}
+
+DITK_EXPORT int ditk_timestep_embedding(const float* t, void* out, int N, int dim, float max_period,
+                                        hipStream_t stream) {
+  DITK_REQUIRE(t && out && N > 0 && dim > 0 && dim % 2 == 0, "ditk_timestep_embedding: bad arguments");
+  int64_t n = (int64_t)N * dim;
+  timestep_embed_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(t, (bf16_t*)out, N, dim, logf(max_period));
+  return ditk_check_launch("ditk_timestep_embedding");
+}
+
+DITK_EXPORT int ditk_cfg_combine(const float* cond, const float* uncond, float* out, int64_t n,
+                                 float guidance, hipStream_t stream) {
+  DITK_REQUIRE(cond && uncond && out && n >= 0, "ditk_cfg_combine: bad arguments");
+  if (n == 0) return 0;
+  cfg_combine_kernel<<<grid_for(n), 256, 0, stream>>>(cond, uncond, out, n, guidance);
+  return ditk_check_launch("ditk_cfg_combine");
+}
+
+DITK_EXPORT int ditk_joint_copy(void* img, int64_t ld_img, void* txt, int64_t ld_txt, void* joint,
+                                int64_t ld_joint, const int32_t* cu_img, const int32_t* cu_txt, int nseg,
+                                int total, int width, int direction, hipStream_t stream) {
+  DITK_REQUIRE(img && txt && joint && cu_img && cu_txt && nseg > 0, "ditk_joint_copy: null argument");
+  DITK_REQUIRE(width % 8 == 0 && ld_img % 8 == 0 && ld_txt % 8 == 0 && ld_joint % 8 == 0,
+               "ditk_joint_copy: widths must be multiples of 8");
+  DITK_REQUIRE(direction == 0 || direction == 1, "ditk_joint_copy: direction must be 0 or 1");
+  if (total == 0) return 0;
+  joint_copy_kernel<<<total, 64, 0, stream>>>((bf16_t*)img, ld_img, (bf16_t*)txt, ld_txt, (bf16_t*)joint,
+                                              ld_joint, cu_img, cu_txt, nseg, total, width, direction);
+  return ditk_check_launch("ditk_joint_copy");
+}
+
+DITK_EXPORT int ditk_silu(const void* x, void* y, int64_t n, hipStream_t stream) {
+  DITK_REQUIRE(x && y && n >= 0, "ditk_silu: bad arguments");
+  if (n == 0) return 0;
+  silu_kernel<<<grid_for(n), 256, 0, stream>>>((const bf16_t*)x, (bf16_t*)y, n);
+  return ditk_check_launch("ditk_silu");
+}

@@ -1,0 +1,242 @@
+// Row-normalisation kernels: fused AdaLN (LayerNorm/RMSNorm + per-segment
+// shift/scale modulation), the modulation table add, and the fused
+// QK-RMSNorm + 3D RoPE kernel.
+//
+// All three are HBM-bound: one wave64 owns one token row, keeps the row in
+// registers (8 bf16 per 16-byte load per lane), reduces with wave shuffles and
+// writes the row once.  Per-token results depend only on the row and its
+// segment's modulation, so packed and per-request runs agree bitwise.
+#include "ditk_common.h"
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
+constexpr int kMaxChunks = 8;     // 16-byte chunks per lane -> D <= 64*8*8 = 4096
+
+// ---------------------------------------------------------------------------
+// AdaLN:  y = norm(x) [* w + b] [* (1 + scale[seg]) + shift[seg]]
+//   norm = LayerNorm (kind 0) or RMSNorm (kind 1), eps inside the rsqrt.
+// ---------------------------------------------------------------------------
+template <int KIND>
+__global__ __launch_bounds__(256) void adaln_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int T, int D,
+    const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
+    const float* __restrict__ scale, int64_t mod_stride, const float* __restrict__ w,
+    const float* __restrict__ b, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const int nchunk = D >> 3;
+  const bf16_t* xr = x + (int64_t)row * ldx;
+  float v[kMaxChunks][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    int c = i * 64 + lane;
+    if (c < nchunk) {
+      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(xr + c * 8);
+      unpack8(raw, v[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[i][j];
+    }
+  }
+  float mean = 0.f;
+  if (KIND == 0) mean = wave_sum<64>(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    int c = i * 64 + lane;
+    if (c < nchunk) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float d = v[i][j] - mean;
+        q = fmaf(d, d, q);
+      }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum<64>(q) / (float)D + eps);
+  const float* sh = nullptr;
+  const float* sc = nullptr;
+  if (shift != nullptr) {
+    int seg = find_segment(cu, nseg, row);
+    sh = shift + (int64_t)seg * mod_stride;
+    sc = scale + (int64_t)seg * mod_stride;
+  }
+  bf16_t* yr = y + (int64_t)row * ldy;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    int c = i * 64 + lane;
+    if (c < nchunk) {
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float n = (v[i][j] - mean) * rstd;
+        int col = c * 8 + j;
+        if (w != nullptr) n = n * w[col];
+        if (b != nullptr) n = n + b[col];
+        if (sh != nullptr) n = n * (1.0f + sc[col]) + sh[col];
+        o[j] = n;
+      }
+      *reinterpret_cast<u32x4_t*>(yr + c * 8) = pack8(o);
+    }
+  }
+}
+
+// mod[s, j, d] = table[j, d] + proj[s, j, d]   (fp32; k rows of D per segment)
+__global__ void modulation_kernel(const float* __restrict__ table, const float* __restrict__ proj,
+                                  float* __restrict__ mod, int nseg, int kd) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t n = (int64_t)nseg * kd;
+  if (i < n) mod[i] = table[i % kd] + proj[i];
+}
+
+// ---------------------------------------------------------------------------
+// QK RMSNorm (+ 3D RoPE), in place.
+//   group == D : RMSNorm across all heads (Wan "rms_norm_across_heads")
+//   group == head_dim : per-head RMSNorm (SD3.5 "rms_norm")
+// RoPE (optional): pair p of each head rotates by the angle of the token's
+// position on the axis that owns p: p < t_pairs -> frame, p < t_pairs+h_pairs
+// -> row, else column.  Angles come from cos/sin tables [max_pos][head_dim/2]
+// built in float64 and rounded to fp32 on the host.
+// Work item: one wave per (token, tensor) with tensor 0 = q, 1 = k.
+// ---------------------------------------------------------------------------
+template <int GROUP_LANES>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    bf16_t* __restrict__ q, int64_t ldq, bf16_t* __restrict__ k, int64_t ldk, int T, int D,
+    int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
+    const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
+    int h_pairs) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (item >= 2 * T) return;
+  const int row = item >> 1;
+  const int which = item & 1;
+  bf16_t* xr = which ? (k + (int64_t)row * ldk) : (q + (int64_t)row * ldq);
+  const float* w = which ? wk : wq;
+  const int nchunk = D >> 3;
+  float v[kMaxChunks][8];
+  float ss[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    int c = i * 64 + lane;
+    ss[i] = 0.f;
+    if (c < nchunk) {
+      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(xr + c * 8);
+      unpack8(raw, v[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[i] = fmaf(v[i][j], v[i][j], ss[i]);
+    }
+  }
+  float rs[kMaxChunks];
+  if (GROUP_LANES == 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) s += ss[i];
+    float r = rsqrtf(wave_sum<64>(s) / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) rs[i] = r;
+  } else {
+    // a head spans GROUP_LANES consecutive lanes of one chunk row
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i)
+      rs[i] = rsqrtf(wave_sum<GROUP_LANES>(ss[i]) / (float)head_dim + eps);
+  }
+  int pf = 0, ph = 0, pw = 0;
+  if (rcos != nullptr) {
+    int seg = find_segment(cu, nseg, row);
+    int s = row - cu[seg];
+    int gh = grids[seg * 3 + 1], gw = grids[seg * 3 + 2];
+    pf = s / (gh * gw);
+    ph = (s / gw) % gh;
+    pw = s % gw;
+    pf = min(pf, max_pos - 1);
+    ph = min(ph, max_pos - 1);
+    pw = min(pw, max_pos - 1);
+  }
+  const int half = head_dim >> 1;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    int c = i * 64 + lane;
+    if (c < nchunk) {
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = v[i][j] * rs[i] * w[c * 8 + j];
+      if (rcos != nullptr) {
+        int d0 = (c * 8) % head_dim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          int p = (d0 >> 1) + j;
+          int pos = p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw);
+          float cs = rcos[pos * half + p];
+          float sn = rsin[pos * half + p];
+          float x1 = o[2 * j], x2 = o[2 * j + 1];
+          o[2 * j] = x1 * cs - x2 * sn;
+          o[2 * j + 1] = x1 * sn + x2 * cs;
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(xr + c * 8) = pack8(o);
+    }
+  }
+}
+
+}  // namespace
+
+DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D,
+                           const int32_t* cu_seqlens, int nseg, const float* shift,
+                           const float* scale, int64_t mod_stride, const float* weight,
+                           const float* bias, float eps, int norm_kind, hipStream_t stream) {
+  DITK_REQUIRE(x != nullptr && y != nullptr, "ditk_adaln: null tensor");
+  DITK_REQUIRE(T >= 0 && D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks,
+               "ditk_adaln: D=%d must be a positive multiple of 8 and <= %d", D, 64 * 8 * kMaxChunks);
+  DITK_REQUIRE(ldx % 8 == 0 && ldy % 8 == 0 && ldx >= D && ldy >= D,
+               "ditk_adaln: leading dims must be multiples of 8 and >= D");
+  DITK_REQUIRE((shift == nullptr) == (scale == nullptr), "ditk_adaln: shift and scale go together");
+  DITK_REQUIRE(shift == nullptr || (cu_seqlens != nullptr && nseg > 0),
+               "ditk_adaln: modulation needs cu_seqlens");
+  DITK_REQUIRE(norm_kind == 0 || norm_kind == 1, "ditk_adaln: norm_kind must be 0 (LN) or 1 (RMS)");
+  if (T == 0) return 0;
+  dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (norm_kind == 0)
+    adaln_kernel<0><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens,
+                                             nseg, shift, scale, mod_stride, weight, bias, eps);
+  else
+    adaln_kernel<1><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens,
+                                             nseg, shift, scale, mod_stride, weight, bias, eps);
+  return ditk_check_launch("ditk_adaln");
+}
+
+DITK_EXPORT int ditk_modulation(const float* table, const float* proj, float* mod, int nseg, int kd,
+                                hipStream_t stream) {
+  DITK_REQUIRE(table && proj && mod && nseg > 0 && kd > 0, "ditk_modulation: bad arguments");
+  int64_t n = (int64_t)nseg * kd;
+  modulation_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(table, proj, mod, nseg, kd);
+  return ditk_check_launch("ditk_modulation");
+}
+
+DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D,
+                                  int head_dim, const float* wq, const float* wk, float eps,
+                                  int per_head, const float* rope_cos, const float* rope_sin,
+                                  int max_pos, const int32_t* cu_seqlens, const int32_t* grids,
+                                  int nseg, int t_pairs, int h_pairs, hipStream_t stream) {
+  DITK_REQUIRE(q && k && wq && wk, "ditk_qk_norm_rope: null tensor");
+  DITK_REQUIRE(D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks, "ditk_qk_norm_rope: bad D=%d", D);
+  DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_qk_norm_rope: head_dim must be 64 or 128");
+  DITK_REQUIRE(D % head_dim == 0, "ditk_qk_norm_rope: D %% head_dim != 0");
+  DITK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0, "ditk_qk_norm_rope: leading dims must be multiples of 8");
+  DITK_REQUIRE(rope_cos == nullptr || (rope_sin && cu_seqlens && grids && nseg > 0 && max_pos > 0),
+               "ditk_qk_norm_rope: RoPE needs tables, cu_seqlens and grids");
+  DITK_REQUIRE(rope_cos == nullptr || (t_pairs >= 0 && h_pairs >= 0 && t_pairs + h_pairs <= head_dim / 2),
+               "ditk_qk_norm_rope: bad axis split");
+  if (T == 0) return 0;
+  dim3 grid((2 * T + kRowsPerBlock - 1) / kRowsPerBlock);
+#define DITK_QKN(G)                                                                             \
+  qk_norm_rope_kernel<G><<<grid, 256, 0, stream>>>((bf16_t*)q, ldq, (bf16_t*)k, ldk, T, D, head_dim, \
+                                                   wq, wk, eps, rope_cos, rope_sin, max_pos,    \
+                                                   cu_seqlens, grids, nseg, t_pairs, h_pairs)
+  if (!per_head) DITK_QKN(64);
+  else if (head_dim == 128) DITK_QKN(16);
+  else DITK_QKN(8);
+#undef DITK_QKN
+  return ditk_check_launch("ditk_qk_norm_rope");
+}

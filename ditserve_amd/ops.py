@@ -1,0 +1,350 @@
+"""Tensor-level wrappers over the ditk C ABI.
+
+Every op validates device, dtype, layout and shape on the host (raising
+ValueError before any launch, as the reference's ``Spec.rejects`` does at
+workers/xfuser/core/attention/spec.py:244-246), allocates outputs with
+``torch.empty`` when none is given, and launches on the caller's current
+stream without synchronising.  There is no CPU or PyTorch fallback.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+EPILOGUES = {"bias": 0, "gelu": 1, "gate_res": 2, "res": 3, "f32": 4, "silu": 5}
+_BF16 = torch.bfloat16
+
+
+def _stream():
+    return ctypes_stream(torch.cuda.current_stream())
+
+
+def ctypes_stream(stream):
+    return _lib.c_void_p(stream.cuda_stream)
+
+
+def _ptr(t):
+    return _lib.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _check(t, name, dtype=None, dims=None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a cuda (HIP) device, got {t.device}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if dims is not None and t.dim() != dims:
+        raise ValueError(f"{name} must be {dims}-D, got shape {tuple(t.shape)}")
+
+
+def _rows(t, name):
+    """2-D row-major view requirements: unit column stride, 16-byte aligned rows."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D tensor with unit column stride, got strides {t.stride()}")
+    if t.stride(0) % 8 or t.data_ptr() % 16:
+        raise ValueError(f"{name} rows must be 16-byte aligned (leading dim % 8 == 0)")
+    return t.stride(0)
+
+
+class Segments:
+    """Packed-batch segment table: host list of offsets + device int32 copy.
+
+    ``cu`` follows build_cu_seqlens (workers/ditserve/models/sd35_batch.py:135-145):
+    [0, n0, n0+n1, ...]."""
+
+    def __init__(self, cu, device):
+        self.cu = [int(x) for x in cu]
+        if not self.cu or self.cu[0] != 0 or any(b < a for a, b in zip(self.cu, self.cu[1:])):
+            raise ValueError(f"cu_seqlens must start at 0 and be nondecreasing, got {self.cu}")
+        self.dev = torch.tensor(self.cu, dtype=torch.int32, device=device)
+
+    @property
+    def nseg(self):
+        return len(self.cu) - 1
+
+    @property
+    def total(self):
+        return self.cu[-1]
+
+    @property
+    def max_len(self):
+        return max(b - a for a, b in zip(self.cu, self.cu[1:]))
+
+    def lengths(self):
+        return [b - a for a, b in zip(self.cu, self.cu[1:])]
+
+
+# ---------------------------------------------------------------------------
+# normalisation
+# ---------------------------------------------------------------------------
+
+def adaln(x, shift=None, scale=None, segments=None, weight=None, bias=None, eps=1e-6, kind="ln", out=None):
+    """y = norm(x)[*w + b][*(1 + scale[seg]) + shift[seg]] -> bf16.
+
+    x [T, D] bf16; shift/scale fp32 views [nseg, D] (row stride may exceed D);
+    weight/bias fp32 [D]; kind "ln" (LayerNorm) or "rms" (RMSNorm)."""
+    _check(x, "x", _BF16, 2)
+    T, D = x.shape
+    ldx = _rows(x, "x")
+    if out is None:
+        out = torch.empty((T, D), dtype=_BF16, device=x.device)
+    ldy = _rows(out, "out")
+    mod_stride = 0
+    cu = None
+    nseg = 0
+    if shift is not None:
+        _check(shift, "shift", torch.float32, 2)
+        _check(scale, "scale", torch.float32, 2)
+        if segments is None:
+            raise ValueError("modulation requires segments")
+        if shift.shape != (segments.nseg, D) or scale.shape != (segments.nseg, D):
+            raise ValueError(f"shift/scale must be [{segments.nseg}, {D}]")
+        if shift.stride(1) != 1 or scale.stride(0) != shift.stride(0):
+            raise ValueError("shift/scale must share a row stride with unit column stride")
+        if segments.total != T:
+            raise ValueError(f"segments cover {segments.total} tokens, x has {T}")
+        mod_stride = shift.stride(0)
+        cu, nseg = segments.dev, segments.nseg
+    for t, n in ((weight, "weight"), (bias, "bias")):
+        if t is not None:
+            _check(t, n, torch.float32, 1)
+            if t.shape[0] != D:
+                raise ValueError(f"{n} must be [{D}]")
+    _lib.call("ditk_adaln", _ptr(x), ldx, _ptr(out), ldy, T, D, _ptr(cu), nseg, _ptr(shift), _ptr(scale),
+              mod_stride, _ptr(weight), _ptr(bias), float(eps), {"ln": 0, "rms": 1}[kind], _stream())
+    return out
+
+
+def modulation(table, proj):
+    """fp32 [nseg, k, D] = table [k, D] + proj [nseg, k, D]  (the reference's
+    ``scale_shift_table + temb.float()``, workers/ditserve/models/wan/block.py:276-280)."""
+    _check(table, "table", torch.float32)
+    _check(proj, "proj", torch.float32)
+    table = table.reshape(-1).contiguous()
+    proj = proj.contiguous()
+    kd = table.numel()
+    if proj.numel() % kd:
+        raise ValueError("proj size is not a multiple of the table size")
+    nseg = proj.numel() // kd
+    out = torch.empty_like(proj)
+    _lib.call("ditk_modulation", _ptr(table), _ptr(proj), _ptr(out), nseg, kd, _stream())
+    return out
+
+
+class Rope:
+    """3D RoPE description for a packed batch: per-axis cos/sin tables
+    [max_pos, head_dim/2] fp32 (float64-built), per-segment (F', H', W') grids."""
+
+    def __init__(self, cos_tab, sin_tab, grids, segments, t_pairs, h_pairs):
+        self.cos, self.sin = cos_tab, sin_tab
+        self.grids = torch.tensor([list(map(int, g)) for g in grids], dtype=torch.int32,
+                                  device=cos_tab.device).reshape(-1)
+        self.segments = segments
+        self.t_pairs, self.h_pairs = int(t_pairs), int(h_pairs)
+        if len(grids) != segments.nseg:
+            raise ValueError("one grid per segment required")
+        for g, n in zip(grids, segments.lengths()):
+            if g[0] * g[1] * g[2] != n:
+                raise ValueError(f"grid {g} does not cover segment of {n} tokens")
+
+
+def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None):
+    """In place: RMSNorm(q), RMSNorm(k) (across all heads, or per head) then 3D RoPE.
+
+    q, k: [T, D] bf16 row views (e.g. column slices of a fused QKV buffer).
+    The reference's `fused_qk_norm_rope` slot contract
+    (workers/xfuser/model_executor/models/transformers/transformer_wan.py:24-25,111-115)."""
+    _check(q, "q", _BF16, 2)
+    _check(k, "k", _BF16, 2)
+    if q.shape != k.shape:
+        raise ValueError("q and k must have the same shape")
+    T, D = q.shape
+    ldq, ldk = _rows(q, "q"), _rows(k, "k")
+    for t, n in ((wq, "wq"), (wk, "wk")):
+        _check(t, n, torch.float32, 1)
+        if t.shape[0] != D:
+            raise ValueError(f"{n} must be [{D}]")
+    if rope is None:
+        args = (None, None, 0, None, None, 0, 0, 0)
+    else:
+        if rope.segments.total != T:
+            raise ValueError("rope segments do not cover q")
+        args = (_ptr(rope.cos), _ptr(rope.sin), rope.cos.shape[0], _ptr(rope.segments.dev), _ptr(rope.grids),
+                rope.segments.nseg, rope.t_pairs, rope.h_pairs)
+    _lib.call("ditk_qk_norm_rope", _ptr(q), ldq, _ptr(k), ldk, T, D, head_dim, _ptr(wq), _ptr(wk), float(eps),
+              int(bool(per_head)), *args, _stream())
+    return q, k
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=None, out=None):
+    """out = epilogue(x @ w.T + b) on MFMA.
+
+    x [M, K] bf16 (row view), w [N, K] bf16, b [N] fp32.  Epilogues: "bias",
+    "gelu" (GELU-tanh), "gate_res" (residual + bf16(y) * gate[seg]), "res"
+    (residual + bf16(y)), "f32" (fp32 output), "silu"."""
+    _check(x, "x", _BF16, 2)
+    _check(w, "w", _BF16, 2)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"weight is {tuple(w.shape)}, input has K={K}")
+    lda, ldw = _rows(x, "x"), _rows(w, "w")
+    if b is not None:
+        _check(b, "bias", torch.float32, 1)
+        if b.shape[0] != N:
+            raise ValueError("bias size mismatch")
+    epi = EPILOGUES[epilogue]
+    odt = torch.float32 if epilogue == "f32" else _BF16
+    if out is None:
+        out = torch.empty((M, N), dtype=odt, device=x.device)
+    _check(out, "out", odt, 2)
+    if out.shape != (M, N) or out.stride(1) != 1 or out.stride(0) % 4:
+        raise ValueError("out must be [M, N] with unit column stride and leading dim % 4 == 0")
+    ldr, gate_stride, cu, nseg = 0, 0, None, 0
+    if epilogue in ("gate_res", "res"):
+        _check(residual, "residual", _BF16, 2)
+        if residual.shape != (M, N) or residual.stride(1) != 1:
+            raise ValueError("residual must be [M, N] row-major")
+        ldr = residual.stride(0)
+    if epilogue == "gate_res":
+        _check(gate, "gate", torch.float32, 2)
+        if segments is None or segments.total != M:
+            raise ValueError("gated epilogue needs segments covering M rows")
+        if gate.shape != (segments.nseg, N) or gate.stride(1) != 1:
+            raise ValueError(f"gate must be [{segments.nseg}, {N}] with unit column stride")
+        gate_stride, cu, nseg = gate.stride(0), segments.dev, segments.nseg
+    _lib.call("ditk_gemm", _ptr(x), lda, _ptr(w), ldw, _ptr(b), _ptr(out), out.stride(0), M, N, K, epi,
+              _ptr(residual), ldr, _ptr(gate), gate_stride, _ptr(cu), nseg, _stream())
+    return out
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def vt_columns(tk, nseg):
+    return int(_lib.load().ditk_vt_columns(int(tk), int(nseg)))
+
+
+def transpose_v(v, heads, head_dim, segments, out=None):
+    """V [Tk, heads*head_dim] -> Vt [heads, head_dim, cols] with per-segment 64-aligned columns."""
+    _check(v, "v", _BF16, 2)
+    ldv = _rows(v, "v")
+    cols = vt_columns(v.shape[0], segments.nseg)
+    if out is None:
+        out = torch.empty((heads, head_dim, cols), dtype=_BF16, device=v.device)
+    _lib.call("ditk_transpose_v", _ptr(v), ldv, _ptr(out), cols, v.shape[0], heads, head_dim,
+              _ptr(segments.dev), segments.nseg, _stream())
+    return out
+
+
+def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None, return_lse=False,
+                      out=None, vt=None):
+    """Block-diagonal varlen attention on packed row views.
+
+    q [Tq, heads*head_dim], k/v [Tk, heads*head_dim] bf16 (row strides may
+    differ, e.g. slices of a fused QKV buffer).  Returns out [Tq, heads*head_dim]
+    (and lse [heads, Tq] fp32, natural log, when return_lse)."""
+    _check(q, "q", _BF16, 2)
+    _check(k, "k", _BF16, 2)
+    width = heads * head_dim
+    if q.shape[1] != width or k.shape[1] != width:
+        raise ValueError(f"q/k must have {width} columns")
+    if seg_q.nseg != seg_k.nseg:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same number of segments")
+    if seg_q.total != q.shape[0] or seg_k.total != k.shape[0]:
+        raise ValueError("cu_seqlens totals must match the packed token counts")
+    ldq, ldk = _rows(q, "q"), _rows(k, "k")
+    if vt is None:
+        _check(v, "v", _BF16, 2)
+        if v.shape != k.shape:
+            raise ValueError("v must match k")
+        vt = transpose_v(v, heads, head_dim, seg_k)
+    Tq = q.shape[0]
+    if out is None:
+        out = torch.empty((Tq, width), dtype=_BF16, device=q.device)
+    ldo = _rows(out, "out")
+    lse = torch.empty((heads, Tq), dtype=torch.float32, device=q.device) if return_lse else None
+    scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
+    _lib.call("ditk_flash_attn_varlen", _ptr(q), ldq, _ptr(k), ldk, _ptr(vt), vt.shape[2], _ptr(out), ldo,
+              _ptr(lse), Tq, _ptr(seg_q.dev), _ptr(seg_k.dev), seg_q.nseg, Tq, heads, head_dim, scale, _stream())
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# prelude / epilogue glue
+# ---------------------------------------------------------------------------
+
+def patchify(latent, patch):
+    """latent [C, F, H, W] bf16 -> [S, C*pt*ph*pw] bf16 (Conv3d-weight feature order)."""
+    _check(latent, "latent", _BF16, 4)
+    latent = latent.contiguous()
+    C, F, H, W = latent.shape
+    pt, ph, pw = patch
+    out = torch.empty(((F // pt) * (H // ph) * (W // pw), C * pt * ph * pw), dtype=_BF16, device=latent.device)
+    _lib.call("ditk_patchify", _ptr(latent), _ptr(out), C, F, H, W, pt, ph, pw, _stream())
+    return out
+
+
+def unpatchify(x, grid, patch, channels):
+    """x [S, pt*ph*pw*C] bf16 -> fp32 latent [C, F'*pt, H'*ph, W'*pw]."""
+    _check(x, "x", _BF16, 2)
+    ldx = x.stride(0)
+    Fp, Hp, Wp = grid
+    pt, ph, pw = patch
+    out = torch.empty((channels, Fp * pt, Hp * ph, Wp * pw), dtype=torch.float32, device=x.device)
+    _lib.call("ditk_unpatchify", _ptr(x), ldx, _ptr(out), channels, Fp, Hp, Wp, pt, ph, pw, _stream())
+    return out
+
+
+def timestep_embedding(t, dim=256, max_period=10000.0):
+    """Sinusoidal [N, dim] bf16, cos half first (flip_sin_to_cos=True, shift 0)."""
+    _check(t, "t", torch.float32)
+    t = t.reshape(-1).contiguous()
+    out = torch.empty((t.numel(), dim), dtype=_BF16, device=t.device)
+    _lib.call("ditk_timestep_embedding", _ptr(t), _ptr(out), t.numel(), dim, float(max_period), _stream())
+    return out
+
+
+def cfg_combine(cond, uncond, guidance):
+    """uncond + g * (cond - uncond), fp32."""
+    _check(cond, "cond", torch.float32)
+    _check(uncond, "uncond", torch.float32)
+    out = torch.empty_like(cond)
+    _lib.call("ditk_cfg_combine", _ptr(cond.contiguous()), _ptr(uncond.contiguous()), _ptr(out), cond.numel(),
+              float(guidance), _stream())
+    return out
+
+
+def joint_gather(img, txt, seg_img, seg_txt, out=None):
+    """Interleave per segment: [img rows of m, txt rows of m] -> joint [Ti+Tt, W]."""
+    total = seg_img.total + seg_txt.total
+    width = img.shape[1]
+    if out is None:
+        out = torch.empty((total, width), dtype=_BF16, device=img.device)
+    _lib.call("ditk_joint_copy", _ptr(img), img.stride(0), _ptr(txt), txt.stride(0), _ptr(out), out.stride(0),
+              _ptr(seg_img.dev), _ptr(seg_txt.dev), seg_img.nseg, total, width, 0, _stream())
+    return out
+
+
+def joint_scatter(joint, img, txt, seg_img, seg_txt):
+    """Inverse of joint_gather: joint rows back into img / txt buffers."""
+    total = seg_img.total + seg_txt.total
+    _lib.call("ditk_joint_copy", _ptr(img), img.stride(0), _ptr(txt), txt.stride(0), _ptr(joint),
+              joint.stride(0), _ptr(seg_img.dev), _ptr(seg_txt.dev), seg_img.nseg, total, joint.shape[1], 1,
+              _stream())
+    return img, txt
+
+
+def silu(x):
+    _check(x, "x", _BF16)
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    _lib.call("ditk_silu", _ptr(x), _ptr(out), x.numel(), _stream())
+    return out

@@ -1,0 +1,149 @@
+/*
+ * ditk — MI355X (gfx950) kernels for ditserve's per-step DiT transformer forward.
+ *
+ * C ABI: plain device pointers, sizes and a hipStream_t (passed as void*).
+ * Every entry point validates its arguments before launching, launches
+ * asynchronously on `stream` (never synchronises), and returns 0 on success or
+ * a nonzero status whose message ditk_last_error() holds (per thread).  bf16
+ * tensors are uint16 arrays, row-major, with explicit leading dimensions in
+ * elements.  cu_seqlens arrays are int32 device arrays [nseg + 1] with
+ * cu[0] = 0 (build_cu_seqlens semantics).
+ *
+ * Reference citations are relative to the zydzydQAQ/ditserve tree.
+ */
+#ifndef DITK_H
+#define DITK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ditk_stream_t; /* hipStream_t */
+
+/* Library version (1). */
+int ditk_version(void);
+
+/* Message of the last failed call on this thread. */
+const char* ditk_last_error(void);
+
+/*
+ * Fused AdaLN:  y = norm(x) [* weight + bias] [* (1 + scale[seg]) + shift[seg]] -> bf16.
+ * norm_kind 0 = LayerNorm (biased variance), 1 = RMSNorm; eps inside rsqrt.
+ * shift/scale: fp32 per segment, row stride mod_stride (may be NULL: no modulation).
+ * weight/bias: fp32 [D] (may be NULL).  In place (y == x) is allowed.
+ * Replaces: Wan AdaLN-1/AdaLN-3 and norm2 — workers/ditserve/models/wan/block.py:283,288,291;
+ *   Wan prediction norm_out — block.py:436-446; SD3.5 packed AdaLN-Zero / AdaLN-Continuous —
+ *   workers/ditserve/models/sd35_batch.py:336-393; Wan cross-attention norm_q/norm_k
+ *   (RMSNorm across heads) — workers/xfuser/model_executor/models/transformers/transformer_wan.py:165-166.
+ */
+int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D, const int32_t* cu_seqlens,
+               int nseg, const float* shift, const float* scale, int64_t mod_stride, const float* weight,
+               const float* bias, float eps, int norm_kind, ditk_stream_t stream);
+
+/*
+ * mod[s, j] = table[j] + proj[s, j] for kd = k*D contiguous fp32 values per segment.
+ * Replaces: _split_temb — workers/ditserve/models/wan/block.py:276-280.
+ */
+int ditk_modulation(const float* table, const float* proj, float* mod, int nseg, int kd, ditk_stream_t stream);
+
+/*
+ * In-place QK RMSNorm (across all heads, or per head when per_head != 0) followed
+ * by 3D RoPE on interleaved pairs (optional: rope_cos == NULL skips it).
+ * rope tables: fp32 [max_pos][head_dim/2]; pair p rotates with the token's frame
+ * position when p < t_pairs, row position when p < t_pairs + h_pairs, else column
+ * position; grids: int32 [nseg][3] = (F', H', W') per segment.
+ * Replaces: _qk_norm_rope_reference and the fused_qk_norm_rope slot —
+ *   transformer_wan.py:24-25,111-115,158-191; SD3.5 per-head norm_q/norm_k —
+ *   sd35_batch.py:426-429,439-442.
+ */
+int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D, int head_dim, const float* wq,
+                      const float* wk, float eps, int per_head, const float* rope_cos, const float* rope_sin,
+                      int max_pos, const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs,
+                      int h_pairs, ditk_stream_t stream);
+
+/*
+ * bf16 MFMA GEMM  C = epilogue(A[M,K] W[N,K]^T + bias[N]) with epilogue
+ *   0 bias, 1 GELU-tanh, 2 gated residual R + bf16(y) * gate[seg] (fp32 math),
+ *   3 residual R + bf16(y), 4 fp32 output, 5 SiLU.
+ * C may alias R.  No split-K: results do not depend on M or on row position.
+ * Replaces: nn.Linear projections of the Wan block (to_q/to_k/to_v/to_out,
+ *   ffn.net.0/ffn.net.2) — transformer_wan.py:50-69,154-155; block.py:285,293;
+ *   SD3.5 packed GEMMs — sd35_batch.py:411-437,696-708; condition/text embedders.
+ */
+int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+              int M, int N, int K, int epilogue, const void* R, int64_t ldr, const float* gate,
+              int64_t gate_stride, const int32_t* cu_seqlens, int nseg, ditk_stream_t stream);
+
+/* Columns of the transposed-V buffer for Tk keys in nseg segments (upper bound). */
+int64_t ditk_vt_columns(int64_t Tk, int nseg);
+
+/*
+ * V [Tk, ldv] (head h at columns h*head_dim) -> Vt [heads][head_dim][vt_ld] with
+ * segment m starting at a 64-aligned column; padding columns are zeroed.
+ * Staging for ditk_flash_attn_varlen (no reference counterpart: the layout change
+ * that feeds V to the MFMA as a K-contiguous operand).
+ */
+int ditk_transpose_v(const void* v, int64_t ldv, void* vt, int64_t vt_ld, int Tk, int heads, int head_dim,
+                     const int32_t* cu_k, int nseg, ditk_stream_t stream);
+
+/*
+ * Varlen block-diagonal flash attention forward (non-causal, no dropout):
+ * segment m's queries [cu_q[m], cu_q[m+1]) attend to keys [cu_k[m], cu_k[m+1]).
+ * head_dim 64 or 128; out bf16 [Tq, heads*head_dim]; lse (optional, may be NULL)
+ * fp32 [heads][lse_ld], natural log of the softmax denominator.
+ * Replaces: the attention backend call Spec.run -> sdpa/aiter kernels —
+ *   workers/xfuser/core/attention/spec.py:283-304, backends/sdpa/kernel.py:30-56,
+ *   backends/aiter/kernel.py:105-128 (via usp.py:815-824 and usp.py:875-908), and the
+ *   SD3.5 varlen slot _FLASH_ATTN_VARLEN_FUNC — sd35_batch.py:19-119,448-486.
+ */
+int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* vt, int64_t vt_ld,
+                           void* o, int64_t ldo, float* lse, int64_t lse_ld, const int32_t* cu_q,
+                           const int32_t* cu_k, int nseg, int Tq, int heads, int head_dim, float softmax_scale,
+                           ditk_stream_t stream);
+
+/*
+ * latent [C, F, H, W] bf16 -> patches [S, C*pt*ph*pw] bf16 (Conv3d weight order).
+ * Replaces: the patch_embedding input gather — transformer_wan.py:328-329.
+ */
+int ditk_patchify(const void* latent, void* out, int C, int F, int H, int W, int pt, int ph, int pw,
+                  ditk_stream_t stream);
+
+/*
+ * x [S, pt*ph*pw*C] bf16 -> fp32 latent [C, F'*pt, H'*ph, W'*pw].
+ * Replaces: prediction's reshape/permute — transformer_wan.py:391-395, block.py:446-448.
+ */
+int ditk_unpatchify(const void* x, int64_t ldx, float* out, int C, int Fp, int Hp, int Wp, int pt, int ph, int pw,
+                    ditk_stream_t stream);
+
+/*
+ * Sinusoidal timestep embedding, bf16 [N, dim], cos half first, frequency shift 0.
+ * Replaces: the Timesteps projection inside condition_embedder — transformer_wan.py:331-333.
+ */
+int ditk_timestep_embedding(const float* t, void* out, int N, int dim, float max_period, ditk_stream_t stream);
+
+/*
+ * out = uncond + guidance * (cond - uncond), fp32.
+ * Replaces: CFG combine — workers/ditserve/models/wan/block.py:483, runtime.py:689, sd35.py:944.
+ */
+int ditk_cfg_combine(const float* cond, const float* uncond, float* out, int64_t n, float guidance,
+                     ditk_stream_t stream);
+
+/*
+ * Joint-sequence copy for SD3.5: direction 0 gathers image and text rows into
+ * joint[cu_img[m] + cu_txt[m] + r] (image rows first), 1 scatters back.
+ * Replaces: index_copy_/index_select — sd35_batch.py:458-463,476-484.
+ */
+int ditk_joint_copy(void* img, int64_t ld_img, void* txt, int64_t ld_txt, void* joint, int64_t ld_joint,
+                    const int32_t* cu_img, const int32_t* cu_txt, int nseg, int total, int width, int direction,
+                    ditk_stream_t stream);
+
+/* y = silu(x), bf16.  Replaces: the SiLU before time_proj / AdaLN linears. */
+int ditk_silu(const void* x, void* y, int64_t n, ditk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DITK_H */

@@ -1,0 +1,275 @@
+"""GPU parity of each ditk kernel against the CPU oracle (fp32 on the same
+bf16-rounded inputs).  Tolerances are stated per test; integer/index work is
+checked bit-exactly, packed-vs-solo runs bitwise."""
+import math
+
+import pytest
+import torch
+
+from oracle import common as oc
+from oracle import wan as ow
+from tests.helpers import assert_close, bf, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ops():
+    from ditserve_amd import ops
+    return ops
+
+
+def _seg(cu):
+    return _ops().Segments(cu, DEV)
+
+
+# --------------------------------------------------------------------------- GEMM
+GEMM_CASES = [(1000, 1536, 1536), (256, 4608, 1536), (77, 64, 1536), (513, 384, 8960), (33, 1536, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_CASES)
+@pytest.mark.parametrize("epi", ["bias", "gelu", "f32", "silu"])
+def test_gemm_epilogues(M, N, K, epi):
+    ops = _ops()
+    a, w, b = bf(randn((M, K), 1)), bf(randn((N, K), 2, 0.02)), bf(randn((N,), 3, 0.1))
+    out = ops.linear(a.to(DEV, torch.bfloat16), w.to(DEV, torch.bfloat16), b.to(DEV), epi).float().cpu()
+    ref = oc.linear(a, w, b)
+    if epi == "gelu":
+        ref = oc.gelu_tanh(ref)
+    elif epi == "silu":
+        ref = oc.silu(ref)
+    # bf16 output rounding bounds the error (2^-9 relative per element)
+    assert_close(out, ref, cos_min=0.99999, rel_max=5e-3, label=f"gemm {epi} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("epi", ["gate_res", "res"])
+def test_gemm_residual_epilogues(epi):
+    ops = _ops()
+    M, N, K = 700, 1536, 1536
+    cu = [0, 300, 650, 700]
+    a, w, b = bf(randn((M, K), 4)), bf(randn((N, K), 5, 0.02)), bf(randn((N,), 6, 0.1))
+    r = bf(randn((M, N), 7))
+    gate = randn((3, N), 8)
+    seg = _seg(cu)
+    out = ops.linear(a.to(DEV, torch.bfloat16), w.to(DEV, torch.bfloat16), b.to(DEV), epi,
+                     residual=r.to(DEV, torch.bfloat16), gate=gate.to(DEV), segments=seg).float().cpu()
+    y = oc.linear(a, w, b)
+    if epi == "gate_res":
+        g = torch.cat([gate[i].expand(cu[i + 1] - cu[i], N) for i in range(3)])
+        ref = r + y * g
+    else:
+        ref = r + y
+    assert_close(out, ref, cos_min=0.99999, rel_max=5e-3, label=epi)
+
+
+def test_gemm_rows_independent_of_packing():
+    """A row's result does not depend on M or on where the row sits (bitwise)."""
+    ops = _ops()
+    K, N = 1536, 1536
+    a = randn((900, K), 9).to(DEV, torch.bfloat16)
+    w = randn((N, K), 10, 0.02).to(DEV, torch.bfloat16)
+    b = randn((N,), 11).to(DEV)
+    full = ops.linear(a, w, b)
+    part = ops.linear(a[313:777].contiguous(), w, b)
+    assert torch.equal(full[313:777], part)
+
+
+# --------------------------------------------------------------------------- AdaLN
+@pytest.mark.parametrize("D", [1536, 3072, 64])
+def test_adaln_modulated_layernorm(D):
+    ops = _ops()
+    cu = [0, 37, 300, 301, 512]
+    T = cu[-1]
+    x = bf(randn((T, D), 12, 3.0) + 0.5)
+    shift, scale = randn((4, D), 13), randn((4, D), 14)
+    out = ops.adaln(x.to(DEV, torch.bfloat16), shift.to(DEV), scale.to(DEV), _seg(cu)).float().cpu()
+    ref = torch.empty(T, D)
+    for m in range(4):
+        s0, s1 = cu[m], cu[m + 1]
+        ref[s0:s1] = oc.layer_norm(x[s0:s1]) * (1 + scale[m]) + shift[m]
+    assert_close(out, ref, cos_min=0.99999, rel_max=5e-3, label=f"adaln D={D}")
+
+
+def test_adaln_affine_and_rms():
+    ops = _ops()
+    T, D = 333, 1536
+    x = bf(randn((T, D), 15, 2.0))
+    w, b = randn((D,), 16, 0.1) + 1, randn((D,), 17, 0.1)
+    out = ops.adaln(x.to(DEV, torch.bfloat16), weight=w.to(DEV), bias=b.to(DEV)).float().cpu()
+    assert_close(out, oc.layer_norm(x, 1e-6, w, b), cos_min=0.99999, rel_max=5e-3, label="ln affine")
+    xd = x.to(DEV, torch.bfloat16)
+    ops.adaln(xd, weight=w.to(DEV), kind="rms", out=xd)  # in place
+    assert_close(xd.float().cpu(), oc.rms_norm(x, w), cos_min=0.99999, rel_max=5e-3, label="rms")
+
+
+# --------------------------------------------------------------------------- QK norm + RoPE
+def test_qk_norm_rope_matches_oracle():
+    ops = _ops()
+    from ditserve_amd.wan import rope_axis_pairs, rope_tables
+    D, H, Dh = 1536, 12, 128
+    grids = [(3, 5, 7), (2, 4, 6), (1, 1, 1)]
+    counts = [f * h * w for f, h, w in grids]
+    cu = [0, counts[0], counts[0] + counts[1], sum(counts)]
+    T = cu[-1]
+    q, k = bf(randn((T, D), 18, 2.0)), bf(randn((T, D), 19, 2.0))
+    wq, wk = bf(randn((D,), 20, 0.1) + 1), bf(randn((D,), 21, 0.1) + 1)
+    seg = _seg(cu)
+    cos_t, sin_t = rope_tables(Dh, 1024, 10000.0, DEV)
+    tp, hp, _ = rope_axis_pairs(Dh)
+    rope = ops.Rope(cos_t, sin_t, grids, seg, tp, hp)
+    qd, kd = q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16)
+    ops.qk_norm_rope_(qd, kd, wq.to(DEV), wk.to(DEV), Dh, rope=rope)
+    for m, g in enumerate(grids):
+        s0, s1 = cu[m], cu[m + 1]
+        cos, sin = ow.rope_freqs(g, Dh)
+        rq, rk = ow.qk_norm_rope(q[s0:s1], k[s0:s1], wq, wk, cos, sin, H)
+        assert_close(qd[s0:s1].float().cpu(), rq.flatten(1), cos_min=0.99999, rel_max=5e-3, label="q")
+        assert_close(kd[s0:s1].float().cpu(), rk.flatten(1), cos_min=0.99999, rel_max=5e-3, label="k")
+
+
+def test_qk_norm_per_head_no_rope():
+    ops = _ops()
+    T, D, Dh = 100, 1536, 64
+    q, k = bf(randn((T, D), 22)), bf(randn((T, D), 23))
+    wq, wk = bf(randn((Dh,), 24, 0.1) + 1), bf(randn((Dh,), 25, 0.1) + 1)
+    qd, kd = q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16)
+    ops.qk_norm_rope_(qd, kd, wq.repeat(D // Dh).to(DEV), wk.repeat(D // Dh).to(DEV), Dh, per_head=True)
+    rq = oc.rms_norm(q.view(T, -1, Dh), wq).flatten(1)
+    assert_close(qd.float().cpu(), rq, cos_min=0.99999, rel_max=5e-3, label="per-head q")
+
+
+# --------------------------------------------------------------------------- attention
+def _attn_case(cu_q, cu_k, H, Dh, seed, scale_in=1.0):
+    q = bf(randn((cu_q[-1], H * Dh), seed, scale_in))
+    k = bf(randn((cu_k[-1], H * Dh), seed + 1, scale_in))
+    v = bf(randn((cu_k[-1], H * Dh), seed + 2))
+    return q, k, v
+
+
+def _attn_ref(q, k, v, cu_q, cu_k, H, Dh):
+    return oc.varlen_attention(q.view(-1, H, Dh), k.view(-1, H, Dh), v.view(-1, H, Dh), cu_q, cu_k).flatten(1)
+
+
+@pytest.mark.parametrize("Dh", [128, 64])
+@pytest.mark.parametrize("lens", [[1], [63], [64], [65, 257], [300, 1, 129, 511], [1025]])
+def test_self_attention_varlen(Dh, lens):
+    ops = _ops()
+    H = 3
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    q, k, v = _attn_case(cu, cu, H, Dh, 30, scale_in=2.0)
+    out, lse = ops.flash_attn_varlen(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16),
+                                     v.to(DEV, torch.bfloat16), _seg(cu), _seg(cu), H, Dh, return_lse=True)
+    ref = _attn_ref(q, k, v, cu, cu, H, Dh)
+    assert_close(out.float().cpu(), ref, cos_min=0.9999, rel_max=1e-2, label=f"self {lens} Dh={Dh}")
+    for m in range(len(lens)):
+        s0, s1 = cu[m], cu[m + 1]
+        qh, kh = q[s0:s1].view(-1, H, Dh).transpose(0, 1), k[s0:s1].view(-1, H, Dh).transpose(0, 1)
+        ref_lse = torch.logsumexp((qh @ kh.transpose(1, 2)) / math.sqrt(Dh), dim=-1)
+        assert torch.allclose(lse[:, s0:s1].cpu(), ref_lse, atol=2e-3, rtol=1e-4)
+
+
+def test_attention_sharp_logits():
+    """Large logits (|s| ~ 30): exercises the running max / rescale path."""
+    ops = _ops()
+    H, Dh, cu = 2, 128, [0, 700, 1500]
+    q, k, v = _attn_case(cu, cu, H, Dh, 40, scale_in=4.0)
+    out = ops.flash_attn_varlen(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), v.to(DEV, torch.bfloat16),
+                                _seg(cu), _seg(cu), H, Dh).float().cpu()
+    assert_close(out, _attn_ref(q, k, v, cu, cu, H, Dh), cos_min=0.999, rel_max=2e-2, label="sharp")
+
+
+@pytest.mark.parametrize("Dh", [128, 64])
+def test_cross_attention_text_blocks(Dh):
+    ops = _ops()
+    H = 4
+    cu_q, cu_k = [0, 900, 1000, 1777], [0, 512, 1024, 1536]
+    q, k, v = _attn_case(cu_q, cu_k, H, Dh, 50)
+    k[512 + 77:1024] = 0  # zero-padded text rows still attend
+    v[512 + 77:1024] = 0
+    out = ops.flash_attn_varlen(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), v.to(DEV, torch.bfloat16),
+                                _seg(cu_q), _seg(cu_k), H, Dh).float().cpu()
+    assert_close(out, _attn_ref(q, k, v, cu_q, cu_k, H, Dh), cos_min=0.9999, rel_max=1e-2, label="cross")
+
+
+def test_attention_packed_equals_solo_bitwise():
+    ops = _ops()
+    H, Dh = 2, 128
+    lens = [300, 1, 513, 64]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    q, k, v = (t.to(DEV, torch.bfloat16) for t in _attn_case(cu, cu, H, Dh, 60))
+    packed = ops.flash_attn_varlen(q, k, v, _seg(cu), _seg(cu), H, Dh)
+    for m in range(len(lens)):
+        s0, s1 = cu[m], cu[m + 1]
+        solo = ops.flash_attn_varlen(q[s0:s1].contiguous(), k[s0:s1].contiguous(), v[s0:s1].contiguous(),
+                                     _seg([0, s1 - s0]), _seg([0, s1 - s0]), H, Dh)
+        assert torch.equal(packed[s0:s1], solo), f"segment {m}"
+
+
+def test_attention_full_length_sampled_rows():
+    """S = 32760 (one Wan2.1 480p request): every K/V tile of the full sequence, checked
+    on 192 sampled query rows against the oracle."""
+    ops = _ops()
+    H, Dh, S = 2, 128, 32760
+    q, k, v = _attn_case([0, S], [0, S], H, Dh, 70)
+    out = ops.flash_attn_varlen(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), v.to(DEV, torch.bfloat16),
+                                _seg([0, S]), _seg([0, S]), H, Dh).float().cpu()
+    rows = torch.cat([torch.arange(0, 64), torch.randint(64, S - 64, (64,), generator=torch.Generator().manual_seed(1)),
+                      torch.arange(S - 64, S)])
+    qs = q[rows].view(-1, H, Dh).transpose(0, 1)
+    ref = oc.sdpa(qs, k.view(S, H, Dh).transpose(0, 1), v.view(S, H, Dh).transpose(0, 1)).transpose(0, 1).flatten(1)
+    assert_close(out[rows], ref, cos_min=0.9999, rel_max=1e-2, label="S=32760 sampled")
+
+
+# --------------------------------------------------------------------------- glue
+def test_patchify_unpatchify_roundtrip_and_oracle():
+    ops = _ops()
+    C, F, H, W = 16, 3, 6, 10
+    lat = bf(randn((C, F, H, W), 80))
+    p = ops.patchify(lat.to(DEV, torch.bfloat16), (1, 2, 2)).float().cpu()
+    ref = lat.reshape(C, F, 1, H // 2, 2, W // 2, 2).permute(1, 3, 5, 0, 2, 4, 6).reshape(F * (H // 2) * (W // 2), -1)
+    assert torch.equal(p, ref)
+    # unpatchify with the (i, j, l, c) feature order of proj_out
+    x = bf(randn((F * (H // 2) * (W // 2), 4 * C), 81))
+    u = ops.unpatchify(x.to(DEV, torch.bfloat16), (F, H // 2, W // 2), (1, 2, 2), C).cpu()
+    ref_u = x.reshape(F, H // 2, W // 2, 1, 2, 2, C).permute(6, 0, 3, 1, 4, 2, 5).reshape(C, F, H, W)
+    assert torch.equal(u, ref_u)
+
+
+def test_timestep_embedding_and_cfg():
+    ops = _ops()
+    t = torch.tensor([0.0, 1.0, 500.0, 999.0])
+    e = ops.timestep_embedding(t.to(DEV), 256).float().cpu()
+    assert_close(e, oc.timestep_embedding(t, 256), cos_min=0.99999, rel_max=5e-3, label="temb")
+    c, u = randn((1000,), 82), randn((1000,), 83)
+    out = ops.cfg_combine(c.to(DEV), u.to(DEV), 5.0).cpu()
+    assert torch.allclose(out, u + 5.0 * (c - u), atol=1e-5)
+
+
+def test_joint_gather_scatter_roundtrip():
+    ops = _ops()
+    img_counts, txt_counts = [40, 7, 100], [33, 33, 33]
+    si, st = _seg([0, 40, 47, 147]), _seg([0, 33, 66, 99])
+    img = randn((147, 128), 84).to(DEV, torch.bfloat16)
+    txt = randn((99, 128), 85).to(DEV, torch.bfloat16)
+    joint = ops.joint_gather(img, txt, si, st)
+    from ditserve_amd.packing import joint_layout
+    lay = joint_layout(img_counts, txt_counts)
+    assert torch.equal(joint[torch.tensor(lay["img_in_joint"], device=DEV)], img)
+    assert torch.equal(joint[torch.tensor(lay["txt_in_joint"], device=DEV)], txt)
+    img2, txt2 = torch.zeros_like(img), torch.zeros_like(txt)
+    ops.joint_scatter(joint, img2, txt2, si, st)
+    assert torch.equal(img2, img) and torch.equal(txt2, txt)
+
+
+def test_invalid_arguments_raise_before_launch():
+    ops = _ops()
+    from ditserve_amd._lib import DitkError
+    x = torch.zeros((10, 96), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises((ValueError, DitkError)):
+        ops.flash_attn_varlen(x, x, x, _seg([0, 10]), _seg([0, 10]), 1, 96)  # head_dim 96 unsupported
+    with pytest.raises(ValueError):
+        ops.linear(x, torch.zeros((8, 64), dtype=torch.bfloat16, device=DEV))  # K mismatch

@@ -1,0 +1,172 @@
+#!/usr/bin/env python3
+"""Benchmark: one Wan2.1-T2V-1.3B denoise step at 480x832x81 frames with CFG batch 2
+(2 x 32760 tokens), bf16, on one MI355X.
+
+A step = packed prelude for the (cond, uncond) pair + 30 DiT blocks + prediction
++ CFG combine + a flow-matching Euler update, all on the ditk HIP kernels.
+Synthetic data: random-init weights N(0, 0.02^2) (norm weights N(1, 0.02^2)),
+latent 16x21x60x104 N(0,1), text contexts 512x4096 N(0,1) with 120 (cond) and 0
+(uncond) valid rows, timestep 999.
+
+Prints one JSON line (rank 0).  `roofline` is for the dominant kernel, the
+self-attention flash kernel, from HIP events recorded on its launch stream over
+the timed steps.  `cpu_baseline` times the oracle (CPU fp32 restatement of the
+reference block) on one full-shape block-forward and extrapolates x60.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0
+LATENT = (16, 21, 60, 104)
+TEXT_VALID = (120, 0)
+TIMESTEP = 999.0
+GUIDANCE = 5.0
+EULER_DT = -1.0 / 50.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--breakdown", action="store_true", help="per-op HIP-event breakdown in the JSON")
+    return ap.parse_args()
+
+
+def cpu_baseline(seq=32760, grid=(21, 30, 52)):
+    """Oracle (CPU fp32, the reference block arithmetic on PyTorch CPU ops) on one
+    full-shape Wan2.1 block-forward; steps/s extrapolated over 30 blocks x 2 branches."""
+    import torch
+
+    from ditserve_amd.wan import WanConfig, random_state_dict
+    from oracle import common as oc
+    from oracle import wan as ow
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    cfg = WanConfig(layers=1)
+    sd = random_state_dict(cfg, seed=0)
+    g = torch.Generator().manual_seed(2)
+    h = torch.randn(seq, cfg.dim, generator=g)
+    enc = torch.randn(cfg.text_len, cfg.dim, generator=g)
+    proj = torch.randn(6, cfg.dim, generator=g) * 0.02
+    cos, sin = ow.rope_freqs(grid)
+    # warm-up on a small slice, then one timed full-shape block
+    ow.block_forward(sd, 0, h[:1560], enc, proj, cos[:1560], sin[:1560], cfg.heads, attn=oc.sdpa_fast)
+    t0 = time.perf_counter()
+    ow.block_forward(sd, 0, h, enc, proj, cos, sin, cfg.heads, attn=oc.sdpa_fast)
+    block_s = time.perf_counter() - t0
+    step_s = block_s * cfg.layers * 2
+    return {
+        "value": 1.0 / step_s,
+        "unit": "steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"1 Wan2.1 block-forward at S={seq} (one CFG branch), fp32, CPU flash SDPA: "
+                  f"{block_s:.2f} s; extrapolated x60 (30 blocks x 2 branches)",
+        "tokens_per_s": 2 * seq / step_s,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); this build "
+              "has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from ditserve_amd import ops
+    from ditserve_amd.profiling import EventProfiler
+    from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer, step_flops
+
+    cfg = WAN21_T2V_1_3B
+    dev = "cuda"
+    model = WanTransformer.random(cfg, seed=0, device=dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    latent = torch.randn(LATENT, generator=g, device=dev)
+    texts = []
+    for valid in TEXT_VALID:
+        t = torch.randn((cfg.text_len, cfg.text_dim), generator=g, device=dev)
+        t[valid:] = 0
+        texts.append(t)
+    seq = (LATENT[1] // cfg.patch[0]) * (LATENT[2] // cfg.patch[1]) * (LATENT[3] // cfg.patch[2])
+
+    def step(lat):
+        cond, uncond = model.forward_packed([lat, lat], [TIMESTEP, TIMESTEP], texts)
+        v = ops.cfg_combine(cond, uncond, GUIDANCE)
+        return lat + EULER_DT * v
+
+    for _ in range(args.warmup):
+        latent = step(latent)
+    torch.cuda.synchronize()
+
+    prof = EventProfiler(enabled=True)
+    model.profiler = prof
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        latent = step(latent)
+    end.record()
+    torch.cuda.synchronize()
+    model.profiler = EventProfiler(enabled=False)
+    if not bool(torch.isfinite(latent).all()):
+        raise RuntimeError("non-finite latent after the timed steps")
+    ms = start.elapsed_time(end) / args.steps
+    regions = prof.summary()
+
+    attn = regions["attn_self"]
+    attn_flops = 4.0 * 2 * seq * seq * cfg.dim  # per launch: 2 segments (CFG pair), non-causal
+    attn_tflops = attn_flops / (attn["avg_ms"] * 1e-3) / 1e12
+    total_flops = step_flops(cfg, [seq, seq], cfg.text_len)
+
+    out = {
+        "metric": METRIC,
+        "value": 1000.0 / ms,
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0,0.02^2), latent/text N(0,1)",
+        "config": {"workload": "Wan2.1-T2V-1.3B-architecture denoise step, latent 16x21x60x104 (480x832x81f), "
+                               "CFG pair packed as 2 x 32760 tokens, 30 blocks, text 512 (valid 120/0), t=999",
+                   "tokens_per_step": 2 * seq, "blocks": cfg.layers},
+        "tokens_per_s": 2 * seq * 1000.0 / ms,
+        "model_tflops": total_flops / (ms * 1e-3) / 1e12,
+        "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "roofline": {
+            "kernel": "flash_fwd_kernel<128> (self-attention, 2 x 32760 tokens x 12 heads)",
+            "bound": "mfma",
+            "achieved": attn_tflops,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": attn_tflops / PEAK_BF16_TFLOPS,
+            "traffic": None,
+            "avg_launch_ms": attn["avg_ms"],
+            "launches": attn["count"],
+            "flops_per_launch": attn_flops,
+        },
+        "reference_a100_steps_per_s": 1000.0 / 3964.62,
+    }
+    if args.breakdown:
+        out["breakdown_ms_per_step"] = {k: v["total_ms"] / args.steps for k, v in regions.items()}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(seq)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -261,7 +261,11 @@ def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None
     if seg_q.total != q.shape[0] or seg_k.total != k.shape[0]:
         raise ValueError("cu_seqlens totals must match the packed token counts")
     ldq, ldk = _rows(q, "q"), _rows(k, "k")
-    if vt is None:
+    if vt is not None:
+        _check(vt, "vt", _BF16, 3)
+        if vt.shape[:2] != (heads, head_dim) or not vt.is_contiguous() or vt.shape[2] < vt_columns(k.shape[0], seg_k.nseg):
+            raise ValueError("vt must be a contiguous [heads, head_dim, >= vt_columns(Tk, nseg)] buffer")
+    else:
         _check(v, "v", _BF16, 2)
         if v.shape != k.shape:
             raise ValueError("v must match k")

@@ -30,6 +30,7 @@ import torch
 
 from . import ops
 from .ops import Segments
+from .profiling import NULL as _NULL_PROFILER
 
 _BF16 = torch.bfloat16
 
@@ -188,6 +189,7 @@ class WanTransformer:
             self.blocks.append(blk)
         self.rope_cos, self.rope_sin = rope_tables(cfg.head_dim, cfg.rope_max_seq_len, cfg.rope_theta, dev)
         self.rope_pairs = rope_axis_pairs(cfg.head_dim)
+        self.profiler = _NULL_PROFILER
 
     @classmethod
     def random(cls, cfg, seed=0, device="cuda"):
@@ -262,31 +264,45 @@ class WanTransformer:
     # -------------------------------------------------------------------- block
     def forward_block(self, packet, index):
         """One block over the packed batch; returns and stores the new hidden."""
-        cfg, blk = self.cfg, self.blocks[index]
+        cfg, blk, prof = self.cfg, self.blocks[index], self.profiler
         D, H, Dh = cfg.dim, cfg.heads, cfg.head_dim
         seg, seg_txt = packet["cu_seqlens_q"], packet["cu_seqlens_kv_text"]
         h = packet["hidden"]
-        mod = ops.modulation(blk["sst"], packet["projected"])  # [R, 6, D] fp32
-        # self-attention (_stage1, block.py:282-285)
-        x = ops.adaln(h, mod[:, 0], mod[:, 1], seg, eps=cfg.eps)
-        qkv = ops.linear(x, blk["qkv_w"], blk["qkv_b"])
+        with prof.region("modulation+adaln"):
+            mod = ops.modulation(blk["sst"], packet["projected"])  # [R, 6, D] fp32
+            # self-attention (_stage1, block.py:282-285)
+            x = ops.adaln(h, mod[:, 0], mod[:, 1], seg, eps=cfg.eps)
+        with prof.region("gemm_qkv"):
+            qkv = ops.linear(x, blk["qkv_w"], blk["qkv_b"])
         q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
-        ops.qk_norm_rope_(q, k, blk["nq1"], blk["nk1"], Dh, cfg.eps, rope=packet["rotary"])
-        a = ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh)
-        h = ops.linear(a, blk["o1_w"], blk["o1_b"], "gate_res", residual=h, gate=mod[:, 2], segments=seg)
+        with prof.region("qk_norm_rope"):
+            ops.qk_norm_rope_(q, k, blk["nq1"], blk["nk1"], Dh, cfg.eps, rope=packet["rotary"])
+        with prof.region("transpose_v"):
+            vt = ops.transpose_v(v, H, Dh, seg)
+        with prof.region("attn_self"):
+            a = ops.flash_attn_varlen(q, k, None, seg, seg, H, Dh, vt=vt)
+        with prof.region("gemm_o_gate"):
+            h = ops.linear(a, blk["o1_w"], blk["o1_b"], "gate_res", residual=h, gate=mod[:, 2], segments=seg)
         # cross-attention (_stage2, block.py:288-290)
-        x = ops.adaln(h, weight=blk["n2_w"], bias=blk["n2_b"], eps=cfg.eps)
-        q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
-        kv2 = ops.linear(packet["encoder"], blk["kv2_w"], blk["kv2_b"])
-        k2, v2 = kv2[:, :D], kv2[:, D:]
-        ops.adaln(q2, weight=blk["nq2"], eps=cfg.eps, kind="rms", out=q2)
-        ops.adaln(k2, weight=blk["nk2"], eps=cfg.eps, kind="rms", out=k2)
-        a = ops.flash_attn_varlen(q2, k2, v2, seg, seg_txt, H, Dh)
-        ops.linear(a, blk["o2_w"], blk["o2_b"], "res", residual=h, out=h)
+        with prof.region("cross_prep"):
+            x = ops.adaln(h, weight=blk["n2_w"], bias=blk["n2_b"], eps=cfg.eps)
+            q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
+            kv2 = ops.linear(packet["encoder"], blk["kv2_w"], blk["kv2_b"])
+            k2, v2 = kv2[:, :D], kv2[:, D:]
+            ops.adaln(q2, weight=blk["nq2"], eps=cfg.eps, kind="rms", out=q2)
+            ops.adaln(k2, weight=blk["nk2"], eps=cfg.eps, kind="rms", out=k2)
+            vt2 = ops.transpose_v(v2, H, Dh, seg_txt)
+        with prof.region("attn_cross"):
+            a = ops.flash_attn_varlen(q2, k2, None, seg, seg_txt, H, Dh, vt=vt2)
+        with prof.region("gemm_o_res"):
+            ops.linear(a, blk["o2_w"], blk["o2_b"], "res", residual=h, out=h)
         # FFN (block.py:291-293)
-        x = ops.adaln(h, mod[:, 3], mod[:, 4], seg, eps=cfg.eps)
-        f = ops.linear(x, blk["f1_w"], blk["f1_b"], "gelu")
-        ops.linear(f, blk["f2_w"], blk["f2_b"], "gate_res", residual=h, gate=mod[:, 5], segments=seg, out=h)
+        with prof.region("modulation+adaln"):
+            x = ops.adaln(h, mod[:, 3], mod[:, 4], seg, eps=cfg.eps)
+        with prof.region("gemm_ffn_up_gelu"):
+            f = ops.linear(x, blk["f1_w"], blk["f1_b"], "gelu")
+        with prof.region("gemm_ffn_down_gate"):
+            ops.linear(f, blk["f2_w"], blk["f2_b"], "gate_res", residual=h, gate=mod[:, 5], segments=seg, out=h)
         packet["hidden"] = h
         return h
 
@@ -295,7 +311,9 @@ class WanTransformer:
         """norm_out AdaLN + proj_out + unpatchify per request -> list of fp32 [C, F, H, W]."""
         cfg = self.cfg
         seg = packet["cu_seqlens_q"]
-        mod = ops.modulation(self.sst_out, packet["temb"].float().reshape(-1, 1, cfg.dim))  # [R, 2, D]
+        # (scale_shift_table [2, D] + temb[:, None]) -> shift, scale   (block.py:441-445)
+        temb = packet["temb"].float().reshape(-1, 1, cfg.dim).expand(-1, 2, -1)
+        mod = ops.modulation(self.sst_out, temb)  # [R, 2, D]
         x = ops.adaln(packet["hidden"], mod[:, 0], mod[:, 1], seg, eps=cfg.eps)
         y = ops.linear(x, self.proj_w, self.proj_b)
         outs = []

@@ -28,8 +28,23 @@
 
 namespace {
 
-constexpr int BM = 256;  // queries per workgroup (4 waves x 64)
 constexpr int BN = 64;   // keys per iteration
+#ifndef ATTN_NW
+#define ATTN_NW 8        // waves per workgroup (32 queries each)
+#endif
+#ifndef ATTN_MINB
+#define ATTN_MINB 1      // workgroups per CU the register budget must allow
+#endif
+#ifndef ATTN_SCHED
+#define ATTN_SCHED 0     // interleave MFMA / VALU / LDS reads with sched_group_barrier
+#endif
+#ifndef ATTN_FENCE
+#define ATTN_FENCE 1     // keep those reads ahead of the MFMAs (scheduling fence)
+#endif
+#ifndef ATTN_PREFETCH
+#define ATTN_PREFETCH 1  // issue a phase's LDS operand reads before its MFMAs
+#endif
+constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 
 // S^T row m of a 32-key MFMA tile holds key kperm(m): with the D layout
 // row = (v/4)*8 + (lane/32)*4 + v%4, this puts key (v/8)*16 + (lane/32)*8 + v%8
@@ -38,12 +53,6 @@ __device__ __forceinline__ int kperm(int m) {
   return ((m >> 4) << 4) | (((m >> 2) & 1) << 3) | (((m >> 3) & 1) << 2) | (m & 3);
 }
 
-template <int HD>
-__device__ __forceinline__ int k_swz(int row, int chunk) {
-  if (HD == 128) return chunk ^ (row & 15);
-  return chunk ^ ((row >> 1) & 7);
-}
-__device__ __forceinline__ int v_swz(int d, int chunk) { return chunk ^ ((d >> 1) & 7); }
 
 // 16 bytes per lane, global -> LDS; the 64 lanes of the wave fill 1 KiB of LDS
 // starting at the wave-uniform `lds_slot0` (lane l writes bytes l*16..l*16+15).
@@ -75,19 +84,34 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
   return pk;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256, 1) void flash_fwd_kernel(
+// LDS tile layouts: rows of 16-byte chunks, grouped 8 chunks (128 B) per row
+// per group, and XOR-swizzled inside the group by the row:
+//   slot(row, u) = (u / 8) * rows * 8 + row * 8 + ((u % 8) ^ ((row >> 1) & 7))
+//   K stage : rows = BN keys, u = head-dim chunk (8 dims each), HD/64 groups
+//   Vt stage: rows = HD dims, u = key chunk (8 keys each), 1 group
+// A DMA instruction fills 64 consecutive slots = 8 rows x 128 contiguous bytes;
+// 16 consecutive lanes reading one chunk of 16 different rows hit 16 distinct
+// 16-byte bank groups; each lane's read address is one of 4 per-lane bases
+// plus a compile-time offset.
+// Pipeline per iteration kt (steady state), per wave:
+//   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) = exp2(S(kt) - m) on VALU
+//   B: O += Vt(kt) P(kt) on MFMA       ||  row max of S(kt+1) on VALU
+// K runs one tile ahead of V through two LDS stages each.
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
     float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
-  constexpr int NC = HD / 16;       // 16-wide k chunks of the head dim
-  constexpr int KCH = HD / 8;       // 16-byte chunks per K row
-  constexpr int K_LOADS = BN * KCH / 256;
-  constexpr int V_LOADS = HD * (BN / 8) / 256;
-  constexpr int DT = HD / 32;       // 32-row d tiles of O^T
+  constexpr int BM = NW * 32;            // queries per workgroup (32 per wave)
+  constexpr int NC = HD / 16;            // 16-wide k chunks of the head dim
+  constexpr int KCH = HD / 8;            // 16-byte chunks per K row
+  constexpr int DT = HD / 32;            // 32-row d tiles of O^T
+  constexpr int K_LOADS = BN * KCH / 64 / NW;   // 64-slot DMA groups per wave
+  constexpr int V_LOADS = HD * 8 / 64 / NW;
+  static_assert(K_LOADS >= 1 && V_LOADS >= 1 && (BN * KCH / 64) % NW == 0, "tile too small for the workgroup");
   __shared__ u32x4_t Ks[2][BN * KCH];
-  __shared__ u32x4_t Vs[2][HD * (BN / 8)];
+  __shared__ u32x4_t Vs[2][HD * 8];
 
   // XCD-aware order: hardware deals workgroup ids round-robin over 8 XCDs, so
   // give each XCD a contiguous run of (head, tile) work — neighbouring query
@@ -103,175 +127,257 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int q_end = cu_q[seg + 1];
-  const int qbase = cu_q[seg] + t * BM + wave * 64;
+  const int qrow = cu_q[seg] + t * BM + wave * 32 + l32;
   const int k_beg = cu_k[seg], k_len = cu_k[seg + 1] - k_beg;
   const int pk = padded_key_start(cu_k, seg);
 
   const bf16_t* Qh = Q + (int64_t)head * HD;
-  const bf16_t* Kh = Kp + (int64_t)head * HD;
+  const bf16_t* Kh = Kp + (int64_t)head * HD + (int64_t)k_beg * ldk;
   const bf16_t* Vh = Vt + (int64_t)head * vt_hs + pk;
 
   // ---- Q fragments (B operand of S^T): lane -> query l32, k-slot hh*8..+8
-  bf16x8_t qf[2][NC];
+  bf16x8_t qf[NC];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    int row = qbase + qt * 32 + l32;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      u32x4_t v = u32x4_t{0, 0, 0, 0};
-      if (row < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)row * ldq + c * 16 + hh * 8);
-      qf[qt][c] = __builtin_bit_cast(bf16x8_t, v);
-    }
+  for (int c = 0; c < NC; ++c) {
+    u32x4_t v = u32x4_t{0, 0, 0, 0};
+    if (qrow < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
+    qf[c] = __builtin_bit_cast(bf16x8_t, v);
   }
 
-  f32x16_t o[DT][2];
+  f32x16_t o[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[d][qt][v] = 0.f;
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+    for (int v = 0; v < 16; ++v) o[d][v] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
 
-  // ---- tile staging: direct global -> LDS 16-byte DMA (no register staging).
-  // Lane l of load instruction i of wave w fills LDS chunk slot
-  // P = (i*4 + w)*64 + l; the XOR swizzle is applied by choosing which global
-  // chunk lands in that slot.  K rows past the segment end read the segment's
-  // last row (finite data; those keys are masked to -inf), Vt padding is zero.
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto issue = [&](int kt, int s) {
+  // ---- DMA (global -> LDS, 16 B per lane).  Instruction i of wave w fills
+  // slots [g*64, g*64 + 64), g = i*NW + w: rows 8*(g%(rows/8)) .. +8 of chunk
+  // group g/(rows/8); lane l -> row + l/8, stored chunk l%8.  The swizzle term of
+  // row (8k + l/8) is ((l >> 4) + 4k) & 7, i.e. one of two per-lane values.
+  // K rows past the segment end re-read its last row; Vt padding is zero.
+  const int lrow = lane >> 3;
+  const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;        // chunk offset, k even
+  const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;  // chunk offset, k odd
+  auto issue_k = [&](int kt, int s) {
     const int kb = kt * BN;
+    const bool full = kb + BN <= k_len;
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
-      const int slot0 = (i * 4 + wave_u) * 64;
-      const int P = slot0 + lane;
-      const int r = P / KCH, ch = k_swz<HD>(r, P % KCH);
-      const int kr = min(kb + r, k_len - 1);
-      lds_dma16(Kh + (int64_t)(k_beg + kr) * ldk + ch * 8, &Ks[s][slot0]);
+      const int g = i * NW + wave_u;
+      const int grp = g / (BN / 8), r8 = g % (BN / 8);
+      int row = r8 * 8 + lrow;
+      if (!full) row = min(row, k_len - kb - 1);
+      const int cho = grp * 64 + ((r8 & 1) ? lsw1 : lsw0);
+      lds_dma16(Kh + (int64_t)(kb + row) * ldk + cho, &Ks[s][g * 64]);
     }
+  };
+  auto issue_v = [&](int kt, int s) {
+    const int kb = kt * BN;
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
-      const int slot0 = (i * 4 + wave_u) * 64;
-      const int P = slot0 + lane;
-      const int d = P >> 3, ch = v_swz(d, P & 7);
-      lds_dma16(Vh + (int64_t)d * vt_ld + kb + ch * 8, &Vs[s][slot0]);
+      const int g = i * NW + wave_u;
+      const int d = g * 8 + lrow;
+      lds_dma16(Vh + (int64_t)d * vt_ld + kb + ((g & 1) ? lsw1 : lsw0), &Vs[s][g * 64]);
     }
   };
 
-  const int nkt = (k_len + BN - 1) / BN;
-  if (nkt > 0) issue(0, 0);
-  dma_wait();
-  __syncthreads();
-
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < nkt) issue(kt + 1, s ^ 1);
-
-    // ---- S^T = K Q^T  (2 key tiles x 2 query tiles)
-    f32x16_t sacc[2][2];
+  // per-lane read bases (slot units): K row kperm(l32), chunk (c%4)*2 + hh;
+  // Vt row l32, chunk (kk*2 + j)*2 + hh.  Both swizzle terms are (row>>1)&7 of
+  // a row whose bits 1..3 come from l32 alone.
+  int kbase[4], vbase[4];
+  {
+    const int kr = kperm(l32), kg = (kr >> 1) & 7, vg = (l32 >> 1) & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kbase[i] = kr * 8 + ((i * 2 + hh) ^ kg);
+      vbase[i] = l32 * 8 + ((i * 2 + hh) ^ vg);
+    }
+  }
+  auto compute_s = [&](int s, f32x16_t (&sacc)[2]) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int v = 0; v < 16; ++v) sacc[kk][v] = 0.f;
+#if ATTN_PREFETCH
+    bf16x8_t kf[NC][2];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[kk][qt][v] = 0.f;
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int r = kk * 32 + kperm(l32);
+      for (int kk = 0; kk < 2; ++kk)
+        kf[c][kk] = __builtin_bit_cast(bf16x8_t, Ks[s][kbase[c & 3] + (c >> 2) * BN * 8 + kk * 256]);
+#if ATTN_FENCE
+    __builtin_amdgcn_sched_barrier(0);
+#endif
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, Ks[s][r * KCH + k_swz<HD>(r, c * 2 + hh)]);
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-          sacc[kk][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qt][c], sacc[kk][qt], 0, 0, 0);
+      for (int kk = 0; kk < 2; ++kk)
+        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c][kk], qf[c], sacc[kk], 0, 0, 0);
+#else
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, Ks[s][kbase[c & 3] + (c >> 2) * BN * 8 + kk * 256]);
+        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], sacc[kk], 0, 0, 0);
       }
+#endif
+  };
+  auto row_max = [&](const f32x16_t (&sacc)[2]) {
+    float a = fmaxf(sacc[0][0], sacc[0][1]), c = fmaxf(sacc[1][0], sacc[1][1]);
+#pragma unroll
+    for (int v = 2; v < 16; v += 2) {
+      a = fmaxf(a, fmaxf(sacc[0][v], sacc[0][v + 1]));
+      c = fmaxf(c, fmaxf(sacc[1][v], sacc[1][v + 1]));
     }
-
-    // ---- online softmax (per lane: one query per query tile)
-    const int valid = k_len - kt * BN;  // keys of this tile that exist
-    uint32_t pf[2][2][2][4];            // [qt][kk][j] 8 bf16 each
+    const float mx = fmaxf(a, c);
+    return fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+  };
+  // lazy rescale: raise the reference max only when a query's tile max exceeds
+  // it by more than 2^kLazy (wave vote); P stays <= 2^kLazy in between.
+  auto maybe_rescale = [&](float mt) {
+    if (__any(mt > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float mx = -INFINITY;
+      for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+    }
+  };
+  // P = exp2(S*c - m) as bf16 B-operand fragments; returns the fp32 row sum
+  // over keys < valid (key of register v in key tile kk: kk*32 + (v/8)*16 + hh*8 + v%8).
+  auto softmax_p = [&](const f32x16_t (&sacc)[2], uint32_t (&pf)[2][2][4], int valid) {
+    const float neg_m = -m_run;
+    float rs = 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          int key = kk * 32 + (v >> 3) * 16 + hh * 8 + (v & 7);
-          float x = sacc[kk][qt][v];
-          if (valid < BN && key >= valid) x = -INFINITY;
-          sacc[kk][qt][v] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qt], mx * scale_log2);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run[qt] - m_use);
-      m_run[qt] = m_new;
-      float rs = 0.f;
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float p0 = exp2f(fmaf(sacc[kk][qt][j * 8 + 2 * e], scale_log2, -m_use));
-            float p1 = exp2f(fmaf(sacc[kk][qt][j * 8 + 2 * e + 1], scale_log2, -m_use));
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e], scale_log2, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e + 1], scale_log2, neg_m));
+          pf[kk][j][e] = pack_bf2(p0, p1);
+          if (valid >= BN) {
             rs += p0 + p1;
-            pf[qt][kk][j][e] = pack_bf2(p0, p1);
+          } else {
+            const int key = kk * 32 + j * 16 + hh * 8 + 2 * e;
+            rs += (key < valid ? p0 : 0.f) + (key + 1 < valid ? p1 : 0.f);
           }
-      l_run[qt] = l_run[qt] * alpha + rs;
-      if (alpha != 1.f) {
+        }
+    return rs;
+  };
+  auto pv = [&](int s, const uint32_t (&pf)[2][2][4]) {
+#if ATTN_PREFETCH
+    bf16x8_t vf[2][2][DT];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int d = 0; d < DT; ++d)
+          vf[kk][j][d] = __builtin_bit_cast(bf16x8_t, Vs[s][vbase[kk * 2 + j] + d * 256]);
+#if ATTN_FENCE
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+#endif
 #pragma unroll
-          for (int v = 0; v < 16; ++v) o[d][qt][v] *= alpha;
-      }
-    }
-
-    // ---- O^T += Vt P^T
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      const int dr = d * 32 + l32;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          bf16x8_t vf = __builtin_bit_cast(bf16x8_t, Vs[s][dr * 8 + v_swz(dr, kk * 4 + j * 2 + hh)]);
-#pragma unroll
-          for (int qt = 0; qt < 2; ++qt) {
-            u32x4_t pv = u32x4_t{pf[qt][kk][j][0], pf[qt][kk][j][1], pf[qt][kk][j][2], pf[qt][kk][j][3]};
-            o[d][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, __builtin_bit_cast(bf16x8_t, pv), o[d][qt], 0, 0, 0);
-          }
+        for (int d = 0; d < DT; ++d) {
+#if ATTN_PREFETCH
+          const bf16x8_t v8 = vf[kk][j][d];
+#else
+          const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, Vs[s][vbase[kk * 2 + j] + d * 256]);
+#endif
+          u32x4_t p4 = u32x4_t{pf[kk][j][0], pf[kk][j][1], pf[kk][j][2], pf[kk][j][3]};
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v8, __builtin_bit_cast(bf16x8_t, p4), o[d], 0, 0, 0);
         }
-    }
+  };
 
+  // Keys past the segment end are clamped duplicates of its last key: they
+  // cannot raise a row max, their Vt columns are zero, and only the final
+  // tile's row sum has to skip them.
+  const int nkt = (k_len + BN - 1) / BN;
+  f32x16_t s_next[2];
+  float mt_next = -INFINITY;
+  if (nkt > 0) {
+    issue_k(0, 0);
+    dma_wait();
+    __syncthreads();
+    compute_s(0, s_next);
+    if (nkt > 1) issue_k(1, 1);
+    issue_v(0, 0);
+    mt_next = row_max(s_next);
     dma_wait();
     __syncthreads();
   }
 
-  // ---- normalise and store
+  // steady state: every tile but the last (all full)
+  for (int kt = 0; kt + 1 < nkt; ++kt) {
+    f32x16_t s_cur[2];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float l = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
-    const int row = qbase + qt * 32 + l32;
-    if (row >= q_end) continue;
+    for (int kk = 0; kk < 2; ++kk) s_cur[kk] = s_next[kk];
+    maybe_rescale(mt_next);
+    const int sk = kt & 1;
+    if (kt + 2 < nkt) issue_k(kt + 2, sk);
+    issue_v(kt + 1, sk ^ 1);
+    uint32_t pf[2][2][4];
+    // phase A: S(kt+1) on MFMA || P(kt) on VALU;  phase B: O += Vt P || max S(kt+1)
+    l_run += softmax_p(s_cur, pf, BN);
+    compute_s(sk ^ 1, s_next);
+    pv(sk, pf);
+    mt_next = row_max(s_next);
+#if ATTN_SCHED
+#pragma unroll
+    for (int i = 0; i < 2 * NC; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // ds_read (K)
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // mfma (S)
+      __builtin_amdgcn_sched_group_barrier(0x002, 112 / (2 * NC), 0);  // valu (softmax)
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * DT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // ds_read (Vt)
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // mfma (PV)
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // valu (row max)
+    }
+#endif
+    dma_wait();
+    __syncthreads();
+  }
+
+  // last tile
+  if (nkt > 0) {
+    maybe_rescale(mt_next);
+    uint32_t pf[2][2][4];
+    l_run += softmax_p(s_next, pf, k_len - (nkt - 1) * BN);
+    pv((nkt - 1) & 1, pf);
+  }
+
+  // ---- normalise and store
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (qrow < q_end) {
     const float inv = (l > 0.f) ? 1.f / l : 0.f;
-    bf16_t* orow = O + (int64_t)row * ldo + (int64_t)head * HD;
+    bf16_t* orow = O + (int64_t)qrow * ldo + (int64_t)head * HD;
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int dd = d * 32 + g * 8 + hh * 4;
-        u32x2_t w = u32x2_t{pack_bf2(o[d][qt][g * 4 + 0] * inv, o[d][qt][g * 4 + 1] * inv),
-                            pack_bf2(o[d][qt][g * 4 + 2] * inv, o[d][qt][g * 4 + 3] * inv)};
+        u32x2_t w = u32x2_t{pack_bf2(o[d][g * 4 + 0] * inv, o[d][g * 4 + 1] * inv),
+                            pack_bf2(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv)};
         *reinterpret_cast<u32x2_t*>(orow + dd) = w;
       }
     if (lse != nullptr && hh == 0)
-      lse[(int64_t)head * lse_ld + row] =
-          (l > 0.f) ? (m_run[qt] + log2f(l)) * 0.6931471805599453f : -INFINITY;
+      lse[(int64_t)head * lse_ld + qrow] = (l > 0.f) ? (m_run + log2f(l)) * 0.6931471805599453f : -INFINITY;
   }
 }
 
@@ -356,19 +462,23 @@ DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k
                ((uintptr_t)o % 8) == 0, "ditk_flash_attn_varlen: misaligned tensor");
   DITK_REQUIRE(softmax_scale > 0.f, "ditk_flash_attn_varlen: softmax_scale must be > 0");
   if (Tq == 0) return 0;
-  const int tiles_bound = (Tq + BM - 1) / BM + nseg;
-  int64_t nblocks = (int64_t)tiles_bound * heads;
-  nblocks = (nblocks + 7) / 8 * 8;
-  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
   const float sl2 = softmax_scale * 1.4426950408889634f;
   const int64_t hs = (int64_t)head_dim * vt_ld;
+  auto run = [&](auto kernel, int bm, int threads) -> int {
+    const int tiles_bound = (Tq + bm - 1) / bm + nseg;
+    int64_t nblocks = (int64_t)tiles_bound * heads;
+    nblocks = (nblocks + 7) / 8 * 8;
+    DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
+    kernel<<<(unsigned)nblocks, threads, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk,
+                                                      (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld,
+                                                      cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+    return 0;
+  };
+  int rc;
   if (head_dim == 128)
-    flash_fwd_kernel<128><<<(unsigned)nblocks, 256, 0, stream>>>(
-        (const bf16_t*)q, ldq, (const bf16_t*)k, ldk, (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse,
-        lse_ld, cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+    rc = run(flash_fwd_kernel<128, ATTN_NW>, ATTN_NW * 32, ATTN_NW * 64);
   else
-    flash_fwd_kernel<64><<<(unsigned)nblocks, 256, 0, stream>>>(
-        (const bf16_t*)q, ldq, (const bf16_t*)k, ldk, (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse,
-        lse_ld, cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+    rc = run(flash_fwd_kernel<64, ATTN_NW>, ATTN_NW * 32, ATTN_NW * 64);
+  if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
 }

@@ -10,10 +10,11 @@
 // features per accumulator group -> 8-byte row-major stores.
 //
 // Tiling (gfx950, v_mfma_f32_32x32x16_bf16): a 256-thread workgroup computes a
-// WG_M (tokens) x WG_N (features) tile with 2x2 waves; K advances in steps of
-// 32 through double-buffered LDS (XOR-swizzled 16-byte chunks, conflict-free
-// for the 32-row operand reads) with the next step's global loads held in
-// registers while the current step's MFMAs run.
+// 256 (tokens) x 256 (features) tile as 2x2 waves of 128x128 (16 accumulator
+// tiles per wave, held in AGPRs).  K advances 64 at a time through
+// double-buffered LDS filled by direct global->LDS DMA (no register staging);
+// inside a stage the operand reads for the next 16-wide k chunk are issued
+// before the current chunk's 16 MFMAs.
 //
 // The k-loop order is fixed and there is no split-K, so every output element is
 // computed the same way whatever M is and wherever its row sits: packed and
@@ -31,152 +32,219 @@ enum Epilogue : int {
   EPI_SILU = 5,      // bf16(silu(bf16(acc + b)))
 };
 
-constexpr int BK = 32;  // k elements per LDS stage (4 x 16-byte chunks per row)
+constexpr int GBM = 256;    // tokens per workgroup tile
+constexpr int GBN = 256;    // features per workgroup tile
+constexpr int GBK = 64;     // k per LDS stage (8 x 16-byte chunks per row)
+constexpr int GROUP_M = 8;  // m-tiles per tile-order group (L2 reuse of W)
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// 16 bytes per lane, global -> LDS; the wave's 64 lanes fill 1 KiB starting at
+// the wave-uniform lds_slot0 (lane l writes bytes 16l .. 16l+15).
+__device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
+                                   (__attribute__((address_space(3))) void*)lds_slot0, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int EPI, int WG_M, int WG_N>
+// LDS stage layout (A and W alike): row r of 64 k-values = 8 chunks of 16 B,
+// slot(r, u) = r*8 + (u ^ ((r >> 1) & 7)).  A DMA instruction fills 64 slots =
+// 8 rows x 128 contiguous bytes; 16 consecutive lanes reading chunk u of 16
+// consecutive rows hit 16 distinct bank groups.
+template <int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
-    const int32_t* __restrict__ cu, int nseg, int tiles_n) {
-  constexpr int TJ = WG_M / 64;  // token MFMA tiles per wave
-  constexpr int TI = WG_N / 64;  // feature MFMA tiles per wave
-  constexpr int A_LOADS = WG_M * 4 / 256;
-  constexpr int W_LOADS = WG_N * 4 / 256;
-  __shared__ u32x4_t As[2][WG_M * 4];
-  __shared__ u32x4_t Ws[2][WG_N * 4];
+    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n) {
+  // 128 KiB of LDS: two stages of A and W tiles; reused by the epilogue as one
+  // 128x128 bf16 staging tile per wave.
+  __shared__ u32x4_t lds[2 * (GBM + GBN) * 8];
+  auto As = [&](int s) { return lds + s * (GBM * 8); };
+  auto Ws = [&](int s) { return lds + 2 * GBM * 8 + s * (GBN * 8); };
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int l32 = lane & 31, h = lane >> 5;
+  // XCD-aware grouped tile order: the 8 XCDs receive workgroup ids round-robin;
+  // give each XCD a contiguous run of logical tiles, ordered in groups of
+  // GROUP_M m-tiles so concurrently running tiles share A rows and W rows in L2.
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int L = (b & 7) * (nb >> 3) + (b >> 3);
+  if (L >= tiles_m * tiles_n) return;
+  const int group = L / (GROUP_M * tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gm = min(GROUP_M, tiles_m - first_m);
+  const int pid = L % (GROUP_M * tiles_n);
+  const int mt = first_m + pid % gm, nt = pid / gm;
+  const int m0 = mt * GBM, n0 = nt * GBN;
 
-  const int tile = blockIdx.x;
-  const int mt = tile / tiles_n, nt = tile % tiles_n;
-  const int m0 = mt * WG_M, n0 = nt * WG_N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave_u & 1, wn = wave_u >> 1;
 
-  // global -> register staging
-  const int ld_row = tid >> 2, ld_chunk = tid & 3;
-  u32x4_t ra[A_LOADS], rw[W_LOADS];
-  const int nk = (K + BK - 1) / BK;
-
-  auto gload = [&](int kt) {
-    const int k = kt * BK + ld_chunk * 8;
+  // ---- DMA source offsets (elements, per lane, loop invariant).  Group g of
+  // 64 slots covers rows 8g..8g+7; lane l -> row 8g + l/8, stored chunk l%8,
+  // k chunk (l%8) ^ (((g&1)*4 + l/16) & 7).  Rows past M / N re-read the last row.
+  const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;
+  const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;
+  const bf16_t* Ablk = A + (int64_t)m0 * lda;
+  const bf16_t* Wblk = W + (int64_t)n0 * ldw;
+  uint32_t a_off[8], w_off[8];  // element offsets within the workgroup's row block
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      int r = m0 + ld_row + i * 64;
-      if (r < M && k < K) ra[i] = *reinterpret_cast<const u32x4_t*>(A + (int64_t)r * lda + k);
-      else ra[i] = u32x4_t{0, 0, 0, 0};
-    }
+  for (int i = 0; i < 8; ++i) {
+    const int g = i * 4 + wave_u;
+    const int row = g * 8 + (lane >> 3);
+    const int sw = (g & 1) ? lsw1 : lsw0;
+    a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + sw);
+    w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + sw);
+  }
+  auto issue = [&](int kt, int s) {
+    const bf16_t* a = Ablk + kt * GBK;
+    const bf16_t* w = Wblk + kt * GBK;
 #pragma unroll
-    for (int i = 0; i < W_LOADS; ++i) {
-      int r = n0 + ld_row + i * 64;
-      if (r < N && k < K) rw[i] = *reinterpret_cast<const u32x4_t*>(W + (int64_t)r * ldw + k);
-      else rw[i] = u32x4_t{0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+      const int g = i * 4 + wave_u;
+      lds_dma16(a + a_off[i], &As(s)[g * 64]);
+      lds_dma16(w + w_off[i], &Ws(s)[g * 64]);
     }
   };
-  auto lstore = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      int r = ld_row + i * 64;
-      As[s][r * 4 + swz(r, ld_chunk)] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < W_LOADS; ++i) {
-      int r = ld_row + i * 64;
-      Ws[s][r * 4 + swz(r, ld_chunk)] = rw[i];
-    }
-  };
 
-  f32x16_t acc[TI][TJ];
+  // ---- operand read bases: row 32t + l32, chunk c*2 + hh (swizzle from l32)
+  int rbase[4];
+  {
+    const int sg = (l32 >> 1) & 7;
 #pragma unroll
-  for (int i = 0; i < TI; ++i)
+    for (int c = 0; c < 4; ++c) rbase[c] = l32 * 8 + ((c * 2 + hh) ^ sg);
+  }
+  const int a_row0 = wm * 128, w_row0 = wn * 128;
+
+  f32x16_t acc[4][4];  // [feature tile i][token tile j]
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  gload(0);
-  lstore(0);
+  const int nk = K / GBK;
+  issue(0, 0);
+  dma_wait();
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
     const int s = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
+    if (kt + 1 < nk) issue(kt + 1, s ^ 1);
+    bf16x8_t af[2][4], bfr[2][4];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      const int chunk = kc * 2 + h;
-      bf16x8_t af[TI], bfr[TJ];
-#pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        int r = wn * (WG_N / 2) + i * 32 + l32;
-        af[i] = __builtin_bit_cast(bf16x8_t, Ws[s][r * 4 + swz(r, chunk)]);
-      }
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        int r = wm * (WG_M / 2) + j * 32 + l32;
-        bfr[j] = __builtin_bit_cast(bf16x8_t, As[s][r * 4 + swz(r, chunk)]);
-      }
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      af[0][i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[0] + (w_row0 + i * 32) * 8]);
+      bfr[0][i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[0] + (a_row0 + i * 32) * 8]);
     }
-    if (kt + 1 < nk) lstore(s ^ 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int cur = c & 1;
+      if (c + 1 < 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          af[cur ^ 1][i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c + 1] + (w_row0 + i * 32) * 8]);
+          bfr[cur ^ 1][i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c + 1] + (a_row0 + i * 32) * 8]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    dma_wait();
     __syncthreads();
   }
 
   // ---------------------------------------------------------------- epilogue
+  // Accumulator lane layout: token t = j*32 + l32 of the wave tile, features
+  // f = i*32 + g*8 + hh*4 + e.
+  if (EPI == EPI_F32) {
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int m = m0 + wm * (WG_M / 2) + j * 32 + l32;
-    if (m >= M) continue;
-    const float* g = nullptr;
-    if (EPI == EPI_GATE_RES) g = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride;
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + a_row0 + j * 32 + l32;
+      if (m >= M) continue;
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + wn * (WG_N / 2) + i * 32 + gq * 8 + h * 4;
-        if (n >= N) continue;
-        float o[4];
+        for (int gq = 0; gq < 4; ++gq) {
+          const int n = n0 + w_row0 + i * 32 + gq * 8 + hh * 4;
+          if (n >= N) continue;
+          float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float t = acc[i][j][gq * 4 + e];
-          if (bias != nullptr) t += bias[n + e];
-          o[e] = t;
-        }
-        if (EPI == EPI_F32) {
+          for (int e = 0; e < 4; ++e) o[e] = acc[i][j][gq * 4 + e] + (bias != nullptr ? bias[n + e] : 0.f);
           float* C = reinterpret_cast<float*>(Cv) + (int64_t)m * ldc + n;
           *reinterpret_cast<f32x4_t*>(C) = f32x4_t{o[0], o[1], o[2], o[3]};
-          continue;
         }
-        if (EPI != EPI_BIAS) {
+    }
+    return;
+  }
+  // bf16 epilogues: y = bf16(acc + bias) goes through a per-wave LDS tile
+  // [128 tokens][128 features] (16-byte chunk c of row t stored at c ^ (t&15)),
+  // then rows are read back so residual / gate loads and output stores are
+  // 16-byte coalesced.
+  u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * 2048);
+  const u32x4_t* stage16 = lds + wave_u * 2048;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = round_bf(o[e]);
-        }
-        if (EPI == EPI_GELU) {
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = gelu_tanh_f(o[e]);
-        } else if (EPI == EPI_SILU) {
+    for (int gq = 0; gq < 4; ++gq) {
+      const int f = i * 32 + gq * 8 + hh * 4;
+      const int n = min(n0 + w_row0 + f, N - 4);
+      float b4[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = silu_f(o[e]);
-        } else if (EPI == EPI_GATE_RES || EPI == EPI_RES) {
-          u32x2_t rr = *reinterpret_cast<const u32x2_t*>(R + (int64_t)m * ldr + n);
-          float rv[4] = {__uint_as_float(rr[0] << 16), __uint_as_float(rr[0] & 0xffff0000u),
-                         __uint_as_float(rr[1] << 16), __uint_as_float(rr[1] & 0xffff0000u)};
+      for (int e = 0; e < 4; ++e) b4[e] = (bias != nullptr) ? bias[n + e] : 0.f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            o[e] = (EPI == EPI_GATE_RES) ? fmaf(o[e], g[n + e], rv[e]) : (rv[e] + o[e]);
-        }
-        bf16_t* C = reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n;
-        *reinterpret_cast<u32x2_t*>(C) = u32x2_t{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+      for (int j = 0; j < 4; ++j) {
+        const int t = j * 32 + l32;
+        const int chunk = (i * 4 + gq) ^ (t & 15);
+        stage8[(t * 16 + chunk) * 2 + hh] =
+            u32x2_t{pack_bf2(acc[i][j][gq * 4 + 0] + b4[0], acc[i][j][gq * 4 + 1] + b4[1]),
+                    pack_bf2(acc[i][j][gq * 4 + 2] + b4[2], acc[i][j][gq * 4 + 3] + b4[3])};
       }
     }
+  __syncthreads();
+  const int c = lane & 15;
+  const int n = n0 + w_row0 + c * 8;
+  if (n >= N) return;
+#pragma unroll 4
+  for (int r = 0; r < 32; ++r) {
+    const int t = r * 4 + (lane >> 4);
+    const int m = m0 + a_row0 + t;
+    if (m >= M) continue;
+    u32x4_t v = stage16[t * 16 + (c ^ (t & 15))];
+    if (EPI != EPI_BIAS) {
+      float x[8];
+      unpack8(v, x);
+      if (EPI == EPI_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = gelu_tanh_f(x[e]);
+      } else if (EPI == EPI_SILU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = silu_f(x[e]);
+      } else {
+        float rv[8];
+        unpack8(*reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n), rv);
+        if (EPI == EPI_GATE_RES) {
+          const float* g = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+          const f32x4_t g0 = *reinterpret_cast<const f32x4_t*>(g);
+          const f32x4_t g1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[e] = fmaf(x[e], g0[e], rv[e]);
+            x[e + 4] = fmaf(x[e + 4], g1[e], rv[e + 4]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = rv[e] + x[e];
+        }
+      }
+      v = pack8(x);
+    }
+    *reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n) = v;
   }
 }
 
@@ -184,11 +252,13 @@ template <int EPI>
 int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
            int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
            int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream) {
-  constexpr int WG_M = 256, WG_N = 128;
-  int tiles_m = (M + WG_M - 1) / WG_M, tiles_n = (N + WG_N - 1) / WG_N;
-  gemm_kernel<EPI, WG_M, WG_N><<<tiles_m * tiles_n, 256, 0, stream>>>(
+  const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int64_t nblocks = (tiles + 7) / 8 * 8;
+  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
+  gemm_kernel<EPI><<<(unsigned)nblocks, 256, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
-      gate_stride, cu, nseg, tiles_n);
+      gate_stride, cu, nseg, tiles_m, tiles_n);
   return ditk_check_launch("ditk_gemm");
 }
 
@@ -200,14 +270,21 @@ DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw
                           const int32_t* cu_seqlens, int nseg, hipStream_t stream) {
   DITK_REQUIRE(A && W && C, "ditk_gemm: null operand");
   DITK_REQUIRE(M >= 0 && N > 0 && K > 0, "ditk_gemm: bad shape M=%d N=%d K=%d", M, N, K);
-  DITK_REQUIRE(K % 8 == 0, "ditk_gemm: K=%d must be a multiple of 8", K);
-  DITK_REQUIRE(N % 4 == 0, "ditk_gemm: N=%d must be a multiple of 4", N);
+  DITK_REQUIRE(K % 64 == 0, "ditk_gemm: K=%d must be a multiple of 64", K);
+  DITK_REQUIRE(N % 8 == 0, "ditk_gemm: N=%d must be a multiple of 8", N);
   DITK_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= K && ldw >= K,
                "ditk_gemm: lda/ldw must be multiples of 8 and >= K");
-  DITK_REQUIRE(ldc % 4 == 0 && ldc >= N, "ditk_gemm: ldc must be a multiple of 4 and >= N");
+  DITK_REQUIRE((int64_t)256 * lda < (1ll << 31) && (int64_t)256 * ldw < (1ll << 31),
+               "ditk_gemm: leading dimensions too large");
+  DITK_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)C % 16) == 0,
+               "ditk_gemm: A, W and C must be 16-byte aligned");
+  DITK_REQUIRE(ldc % 8 == 0 && ldc >= N, "ditk_gemm: ldc must be a multiple of 8 and >= N");
   DITK_REQUIRE(epilogue >= 0 && epilogue <= 5, "ditk_gemm: unknown epilogue %d", epilogue);
-  DITK_REQUIRE(!(epilogue == EPI_GATE_RES || epilogue == EPI_RES) || (R && ldr % 4 == 0 && ldr >= N),
-               "ditk_gemm: residual epilogue needs R with ldr %% 4 == 0");
+  DITK_REQUIRE(!(epilogue == EPI_GATE_RES || epilogue == EPI_RES) ||
+               (R && ldr % 8 == 0 && ldr >= N && ((uintptr_t)R % 16) == 0),
+               "ditk_gemm: residual epilogue needs a 16-byte aligned R with ldr %% 8 == 0");
+  DITK_REQUIRE(epilogue != EPI_GATE_RES || (gate_stride % 4 == 0 && ((uintptr_t)gate % 16) == 0),
+               "ditk_gemm: gate rows must be 16-byte aligned");
   DITK_REQUIRE(epilogue != EPI_GATE_RES || (gate && cu_seqlens && nseg > 0),
                "ditk_gemm: gated epilogue needs gate and cu_seqlens");
   if (M == 0) return 0;

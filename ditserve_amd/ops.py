@@ -204,20 +204,22 @@ def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=Non
     if out is None:
         out = torch.empty((M, N), dtype=odt, device=x.device)
     _check(out, "out", odt, 2)
-    if out.shape != (M, N) or out.stride(1) != 1 or out.stride(0) % 4:
-        raise ValueError("out must be [M, N] with unit column stride and leading dim % 4 == 0")
+    if out.shape != (M, N) or out.stride(1) != 1 or out.stride(0) % 8 or out.data_ptr() % 16:
+        raise ValueError("out must be [M, N], unit column stride, leading dim % 8 == 0, 16-byte aligned")
+    if N % 8 or K % 64:
+        raise ValueError(f"linear needs N % 8 == 0 and K % 64 == 0 (got N={N}, K={K})")
     ldr, gate_stride, cu, nseg = 0, 0, None, 0
     if epilogue in ("gate_res", "res"):
         _check(residual, "residual", _BF16, 2)
-        if residual.shape != (M, N) or residual.stride(1) != 1:
-            raise ValueError("residual must be [M, N] row-major")
+        if residual.shape != (M, N) or residual.stride(1) != 1 or residual.stride(0) % 8 or residual.data_ptr() % 16:
+            raise ValueError("residual must be [M, N] row-major with 16-byte aligned rows")
         ldr = residual.stride(0)
     if epilogue == "gate_res":
         _check(gate, "gate", torch.float32, 2)
         if segments is None or segments.total != M:
             raise ValueError("gated epilogue needs segments covering M rows")
-        if gate.shape != (segments.nseg, N) or gate.stride(1) != 1:
-            raise ValueError(f"gate must be [{segments.nseg}, {N}] with unit column stride")
+        if gate.shape != (segments.nseg, N) or gate.stride(1) != 1 or gate.stride(0) % 4 or gate.data_ptr() % 16:
+            raise ValueError(f"gate must be [{segments.nseg}, {N}] with unit column stride and 16-byte aligned rows")
         gate_stride, cu, nseg = gate.stride(0), segments.dev, segments.nseg
     _lib.call("ditk_gemm", _ptr(x), lda, _ptr(w), ldw, _ptr(b), _ptr(out), out.stride(0), M, N, K, epi,
               _ptr(residual), ldr, _ptr(gate), gate_stride, _ptr(cu), nseg, _stream())

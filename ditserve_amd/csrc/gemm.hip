@@ -12,9 +12,9 @@
 // Tiling (gfx950, v_mfma_f32_32x32x16_bf16): a 256-thread workgroup computes a
 // 256 (tokens) x 256 (features) tile as 2x2 waves of 128x128 (16 accumulator
 // tiles per wave, held in AGPRs).  K advances 64 at a time through
-// double-buffered LDS filled by direct global->LDS DMA (no register staging);
-// inside a stage the operand reads for the next 16-wide k chunk are issued
-// before the current chunk's 16 MFMAs.
+// NSTAGE LDS stages (32 k each) filled by direct global->LDS DMA, with three
+// stages in flight to cover memory latency (no register staging); each
+// stage's operand reads are issued together before its 32 MFMAs.
 //
 // The k-loop order is fixed and there is no split-K, so every output element is
 // computed the same way whatever M is and wherever its row sits: packed and
@@ -34,7 +34,9 @@ enum Epilogue : int {
 
 constexpr int GBM = 256;    // tokens per workgroup tile
 constexpr int GBN = 256;    // features per workgroup tile
-constexpr int GBK = 64;     // k per LDS stage (8 x 16-byte chunks per row)
+constexpr int GBK = 32;     // k per LDS stage (4 x 16-byte chunks per row)
+constexpr int NSTAGE = 4;   // LDS stages: 3 k-steps of DMA in flight
+
 constexpr int GROUP_M = 8;  // m-tiles per tile-order group (L2 reuse of W)
 
 // 16 bytes per lane, global -> LDS; the wave's 64 lanes fill 1 KiB starting at
@@ -43,11 +45,16 @@ __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
                                    (__attribute__((address_space(3))) void*)lds_slot0, 16, 0, 0);
 }
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// wait until at most n (0, 8 or 16) of this wave's DMA instructions are in flight
+__device__ __forceinline__ void dma_wait_le(int n) {
+  if (n >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
-// LDS stage layout (A and W alike): row r of 64 k-values = 8 chunks of 16 B,
-// slot(r, u) = r*8 + (u ^ ((r >> 1) & 7)).  A DMA instruction fills 64 slots =
-// 8 rows x 128 contiguous bytes; 16 consecutive lanes reading chunk u of 16
+// LDS stage layout (A and W alike): row r of 32 k-values = 4 chunks of 16 B,
+// slot(r, u) = r*4 + (u ^ ((r >> 2) & 3)).  A DMA instruction fills 64 slots =
+// 16 rows x 64 contiguous bytes; 16 consecutive lanes reading chunk u of 16
 // consecutive rows hit 16 distinct bank groups.
 template <int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(
@@ -55,11 +62,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n) {
-  // 128 KiB of LDS: two stages of A and W tiles; reused by the epilogue as one
-  // 128x128 bf16 staging tile per wave.
-  __shared__ u32x4_t lds[2 * (GBM + GBN) * 8];
-  auto As = [&](int s) { return lds + s * (GBM * 8); };
-  auto Ws = [&](int s) { return lds + 2 * GBM * 8 + s * (GBN * 8); };
+  // 128 KiB of LDS: NSTAGE stages of A and W tiles; reused by the epilogue as
+  // one 128x128 bf16 staging tile per wave.
+  __shared__ u32x4_t lds[NSTAGE * (GBM + GBN) * 4];
+  auto As = [&](int s) { return lds + s * (GBM * 4); };
+  auto Ws = [&](int s) { return lds + NSTAGE * GBM * 4 + s * (GBN * 4); };
 
   // XCD-aware grouped tile order: the 8 XCDs receive workgroup ids round-robin;
   // give each XCD a contiguous run of logical tiles, ordered in groups of
@@ -80,26 +87,25 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   const int wm = wave_u & 1, wn = wave_u >> 1;
 
   // ---- DMA source offsets (elements, per lane, loop invariant).  Group g of
-  // 64 slots covers rows 8g..8g+7; lane l -> row 8g + l/8, stored chunk l%8,
-  // k chunk (l%8) ^ (((g&1)*4 + l/16) & 7).  Rows past M / N re-read the last row.
-  const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;
-  const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;
+  // 64 slots covers rows 16g..16g+15; lane l -> row 16g + l/4, stored chunk
+  // l%4, k chunk (l%4) ^ ((l>>4)&3).  Rows past M / N re-read the last row.
   const bf16_t* Ablk = A + (int64_t)m0 * lda;
   const bf16_t* Wblk = W + (int64_t)n0 * ldw;
-  uint32_t a_off[8], w_off[8];  // element offsets within the workgroup's row block
+  const int lsw = ((lane & 3) ^ ((lane >> 4) & 3)) * 8;
+  uint32_t a_off[4], w_off[4];  // element offsets within the workgroup's row block
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int g = i * 4 + wave_u;
-    const int row = g * 8 + (lane >> 3);
-    const int sw = (g & 1) ? lsw1 : lsw0;
-    a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + sw);
-    w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + sw);
+    const int row = g * 16 + (lane >> 2);
+    a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + lsw);
+    w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + lsw);
   }
-  auto issue = [&](int kt, int s) {
+  auto issue = [&](int kt) {
+    const int s = kt % NSTAGE;
     const bf16_t* a = Ablk + kt * GBK;
     const bf16_t* w = Wblk + kt * GBK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int g = i * 4 + wave_u;
       lds_dma16(a + a_off[i], &As(s)[g * 64]);
       lds_dma16(w + w_off[i], &Ws(s)[g * 64]);
@@ -107,11 +113,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   };
 
   // ---- operand read bases: row 32t + l32, chunk c*2 + hh (swizzle from l32)
-  int rbase[4];
+  int rbase[2];
   {
-    const int sg = (l32 >> 1) & 7;
+    const int sg = (l32 >> 2) & 3;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) rbase[c] = l32 * 8 + ((c * 2 + hh) ^ sg);
+    for (int c = 0; c < 2; ++c) rbase[c] = l32 * 4 + ((c * 2 + hh) ^ sg);
   }
   const int a_row0 = wm * 128, w_row0 = wn * 128;
 
@@ -124,40 +130,87 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int nk = K / GBK;
-  issue(0, 0);
-  dma_wait();
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < nk) issue(kt + 1, s ^ 1);
-    bf16x8_t af[2][4], bfr[2][4];
+  auto read_chunk = [&](int s, int c, bf16x8_t (&af)[4], bf16x8_t (&bf)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      af[0][i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[0] + (w_row0 + i * 32) * 8]);
-      bfr[0][i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[0] + (a_row0 + i * 32) * 8]);
+      af[i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + i * 32) * 4]);
+      bf[i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + i * 32) * 4]);
     }
+  };
+  auto mfma_chunk = [&](const bf16x8_t (&af)[4], const bf16x8_t (&bf)[4]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int cur = c & 1;
-      if (c + 1 < 4) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          af[cur ^ 1][i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c + 1] + (w_row0 + i * 32) * 8]);
-          bfr[cur ^ 1][i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c + 1] + (a_row0 + i * 32) * 8]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  };
+
+  // Pipeline: stages kt+1..kt+3 of DMA in flight; the barrier that publishes
+  // stage kt+1 and the first operand reads from it sit between the two MFMA
+  // batches of stage kt, so the MFMA pipe keeps draining through them.  Every
+  // wave waits for its own DMA with vmcnt before the barrier, so a plain
+  // s_barrier (no release fence, which would drain all stages in flight)
+  // publishes the stage.
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+  for (int kt = 0; kt < NSTAGE - 1; ++kt)
+    if (kt < nk) issue(kt);
+  bf16x8_t fa0[4], fb0[4], fa1[4], fb1[4];
+  dma_wait_le(8 * min(NSTAGE - 2, nk - 1));
+  __syncthreads();
+  read_chunk(0, 0, fa0, fb0);
+
+  auto publish = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+  int kt = 0;
+  // steady state: a DMA stage to issue every iteration.  The MFMAs, the next
+  // operand reads and the DMA issues are interleaved in fixed groups (2 MFMA,
+  // 1 ds_read, 1 DMA) fenced by sched_barrier, so DMA issue never stalls a
+  // long run of MFMAs.
+  for (; kt + NSTAGE - 1 < nk; ++kt) {
+    const int s = kt % NSTAGE;
+    const int sn = (kt + NSTAGE - 1) % NSTAGE;
+    const bf16_t* an = Ablk + (kt + NSTAGE - 1) * GBK;
+    const bf16_t* wn_ = Wblk + (kt + NSTAGE - 1) * GBK;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+    for (int q = 0; q < 8; ++q) {
+      // 2 MFMAs of chunk 0, one operand read of chunk 1, one DMA of stage kt+3
+      const int i0 = (2 * q) / 4, j0 = (2 * q) % 4;
+      acc[i0][j0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[i0], fb0[j0], acc[i0][j0], 0, 0, 0);
+      acc[i0][j0 + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[i0], fb0[j0 + 1], acc[i0][j0 + 1], 0, 0, 0);
+      if (q < 4) fa1[q] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[1] + (w_row0 + q * 32) * 4]);
+      else fb1[q - 4] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[1] + (a_row0 + (q - 4) * 32) * 4]);
+      const int g = (q >> 1) * 4 + wave_u;
+      if ((q & 1) == 0) lds_dma16(an + a_off[q >> 1], &As(sn)[g * 64]);
+      else lds_dma16(wn_ + w_off[q >> 1], &Ws(sn)[g * 64]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    dma_wait();
-    __syncthreads();
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // stage kt+1 landed (this wave)
+    publish();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i0 = (2 * q) / 4, j0 = (2 * q) % 4;
+      acc[i0][j0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[i0], fb1[j0], acc[i0][j0], 0, 0, 0);
+      acc[i0][j0 + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[i0], fb1[j0 + 1], acc[i0][j0 + 1], 0, 0, 0);
+      if (q < 4) fa0[q] = __builtin_bit_cast(bf16x8_t, Ws((kt + 1) % NSTAGE)[rbase[0] + (w_row0 + q * 32) * 4]);
+      else fb0[q - 4] = __builtin_bit_cast(bf16x8_t, As((kt + 1) % NSTAGE)[rbase[0] + (a_row0 + (q - 4) * 32) * 4]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  // drain: no more DMA to issue
+  for (; kt < nk; ++kt) {
+    const int s = kt % NSTAGE;
+    read_chunk(s, 1, fa1, fb1);
+    mfma_chunk(fa0, fb0);
+    if (kt + 1 < nk) {
+      dma_wait_le(8 * (nk - 2 - kt));
+      publish();
+      read_chunk((kt + 1) % NSTAGE, 0, fa0, fb0);
+    }
+    mfma_chunk(fa1, fb1);
+  }
+  __syncthreads();
 
   // ---------------------------------------------------------------- epilogue
   // Accumulator lane layout: token t = j*32 + l32 of the wave tile, features
@@ -188,6 +241,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   // 16-byte coalesced.
   u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * 2048);
   const u32x4_t* stage16 = lds + wave_u * 2048;
+  static_assert(NSTAGE * (GBM + GBN) * 4 >= 4 * 2048, "epilogue staging needs 128 KiB");
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -270,7 +324,7 @@ DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw
                           const int32_t* cu_seqlens, int nseg, hipStream_t stream) {
   DITK_REQUIRE(A && W && C, "ditk_gemm: null operand");
   DITK_REQUIRE(M >= 0 && N > 0 && K > 0, "ditk_gemm: bad shape M=%d N=%d K=%d", M, N, K);
-  DITK_REQUIRE(K % 64 == 0, "ditk_gemm: K=%d must be a multiple of 64", K);
+  DITK_REQUIRE(K % 32 == 0, "ditk_gemm: K=%d must be a multiple of 32", K);
   DITK_REQUIRE(N % 8 == 0, "ditk_gemm: N=%d must be a multiple of 8", N);
   DITK_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= K && ldw >= K,
                "ditk_gemm: lda/ldw must be multiples of 8 and >= K");

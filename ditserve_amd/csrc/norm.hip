@@ -63,19 +63,39 @@ __global__ __launch_bounds__(256) void adaln_kernel(
     sc = scale + (int64_t)seg * mod_stride;
   }
   bf16_t* yr = y + (int64_t)row * ldy;
+  // per-column vectors are read as two 16-byte loads per 8-column chunk
+  auto load8 = [](const float* p, float* out) {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[j] = a[j];
+      out[j + 4] = b[j];
+    }
+  };
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {
     int c = i * 64 + lane;
     if (c < nchunk) {
-      float o[8];
+      float o[8], t[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float n = (v[i][j] - mean) * rstd;
-        int col = c * 8 + j;
-        if (w != nullptr) n = n * w[col];
-        if (b != nullptr) n = n + b[col];
-        if (sh != nullptr) n = n * (1.0f + sc[col]) + sh[col];
-        o[j] = n;
+      for (int j = 0; j < 8; ++j) o[j] = (v[i][j] - mean) * rstd;
+      if (w != nullptr) {
+        load8(w + c * 8, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] *= t[j];
+      }
+      if (b != nullptr) {
+        load8(b + c * 8, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += t[j];
+      }
+      if (sh != nullptr) {
+        float u[8];
+        load8(sc + c * 8, t);
+        load8(sh + c * 8, u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = o[j] * (1.0f + t[j]) + u[j];
       }
       *reinterpret_cast<u32x4_t*>(yr + c * 8) = pack8(o);
     }
@@ -160,17 +180,30 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     int c = i * 64 + lane;
     if (c < nchunk) {
       float o[8];
+      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(w + c * 8);
+      const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(w + c * 8 + 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = v[i][j] * rs[i] * w[c * 8 + j];
+      for (int j = 0; j < 4; ++j) {
+        o[j] = v[i][j] * rs[i] * w0[j];
+        o[j + 4] = v[i][j + 4] * rs[i] * w1[j];
+      }
       if (rcos != nullptr) {
-        int d0 = (c * 8) % head_dim;
+        // pairs p0..p0+3 of this chunk; they belong to at most two axes, so
+        // read 16 bytes from the table row of the first and of the last pair.
+        const int p0 = ((c * 8) % head_dim) >> 1;
+        auto axis_pos = [&](int p) { return p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw); };
+        const int pa = axis_pos(p0), pb = axis_pos(p0 + 3);
+        const f32x4_t ca = *reinterpret_cast<const f32x4_t*>(rcos + pa * half + p0);
+        const f32x4_t sa = *reinterpret_cast<const f32x4_t*>(rsin + pa * half + p0);
+        const f32x4_t cb = *reinterpret_cast<const f32x4_t*>(rcos + pb * half + p0);
+        const f32x4_t sb = *reinterpret_cast<const f32x4_t*>(rsin + pb * half + p0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          int p = (d0 >> 1) + j;
-          int pos = p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw);
-          float cs = rcos[pos * half + p];
-          float sn = rsin[pos * half + p];
-          float x1 = o[2 * j], x2 = o[2 * j + 1];
+          const bool first = (p0 + j < t_pairs) == (p0 < t_pairs) &&
+                             (p0 + j < t_pairs + h_pairs) == (p0 < t_pairs + h_pairs);
+          const float cs = first ? ca[j] : cb[j];
+          const float sn = first ? sa[j] : sb[j];
+          const float x1 = o[2 * j], x2 = o[2 * j + 1];
           o[2 * j] = x1 * cs - x2 * sn;
           o[2 * j + 1] = x1 * sn + x2 * cs;
         }
@@ -192,6 +225,10 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
   DITK_REQUIRE(ldx % 8 == 0 && ldy % 8 == 0 && ldx >= D && ldy >= D,
                "ditk_adaln: leading dims must be multiples of 8 and >= D");
   DITK_REQUIRE((shift == nullptr) == (scale == nullptr), "ditk_adaln: shift and scale go together");
+  DITK_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0, "ditk_adaln: x and y must be 16-byte aligned");
+  DITK_REQUIRE(((uintptr_t)shift % 16) == 0 && ((uintptr_t)scale % 16) == 0 && mod_stride % 4 == 0 &&
+               ((uintptr_t)weight % 16) == 0 && ((uintptr_t)bias % 16) == 0,
+               "ditk_adaln: modulation / affine vectors must be 16-byte aligned");
   DITK_REQUIRE(shift == nullptr || (cu_seqlens != nullptr && nseg > 0),
                "ditk_adaln: modulation needs cu_seqlens");
   DITK_REQUIRE(norm_kind == 0 || norm_kind == 1, "ditk_adaln: norm_kind must be 0 (LN) or 1 (RMS)");
@@ -224,10 +261,16 @@ DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, in
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_qk_norm_rope: head_dim must be 64 or 128");
   DITK_REQUIRE(D % head_dim == 0, "ditk_qk_norm_rope: D %% head_dim != 0");
   DITK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0, "ditk_qk_norm_rope: leading dims must be multiples of 8");
+  DITK_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)wq % 16) == 0 &&
+               ((uintptr_t)wk % 16) == 0, "ditk_qk_norm_rope: tensors must be 16-byte aligned");
   DITK_REQUIRE(rope_cos == nullptr || (rope_sin && cu_seqlens && grids && nseg > 0 && max_pos > 0),
                "ditk_qk_norm_rope: RoPE needs tables, cu_seqlens and grids");
   DITK_REQUIRE(rope_cos == nullptr || (t_pairs >= 0 && h_pairs >= 0 && t_pairs + h_pairs <= head_dim / 2),
                "ditk_qk_norm_rope: bad axis split");
+  DITK_REQUIRE(rope_cos == nullptr || h_pairs == 0 || h_pairs >= 4,
+               "ditk_qk_norm_rope: the middle axis must own 0 or >= 4 pairs");
+  DITK_REQUIRE(rope_cos == nullptr || (((uintptr_t)rope_cos % 16) == 0 && ((uintptr_t)rope_sin % 16) == 0),
+               "ditk_qk_norm_rope: RoPE tables must be 16-byte aligned");
   if (T == 0) return 0;
   dim3 grid((2 * T + kRowsPerBlock - 1) / kRowsPerBlock);
 #define DITK_QKN(G)                                                                             \

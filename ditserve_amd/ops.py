@@ -206,8 +206,8 @@ def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=Non
     _check(out, "out", odt, 2)
     if out.shape != (M, N) or out.stride(1) != 1 or out.stride(0) % 8 or out.data_ptr() % 16:
         raise ValueError("out must be [M, N], unit column stride, leading dim % 8 == 0, 16-byte aligned")
-    if N % 8 or K % 64:
-        raise ValueError(f"linear needs N % 8 == 0 and K % 64 == 0 (got N={N}, K={K})")
+    if N % 8 or K % 32:
+        raise ValueError(f"linear needs N % 8 == 0 and K % 32 == 0 (got N={N}, K={K})")
     ldr, gate_stride, cu, nseg = 0, 0, None, 0
     if epilogue in ("gate_res", "res"):
         _check(residual, "residual", _BF16, 2)

@@ -59,14 +59,28 @@ class Segments:
         if not self.cu or self.cu[0] != 0 or any(b < a for a, b in zip(self.cu, self.cu[1:])):
             raise ValueError(f"cu_seqlens must start at 0 and be nondecreasing, got {self.cu}")
         self.dev = torch.tensor(self.cu, dtype=torch.int32, device=device)
+        self._nseg, self._total = len(self.cu) - 1, self.cu[-1]
+
+    @classmethod
+    def from_device(cls, cu_dev, total):
+        """Wrap a device int32 cu_seqlens tensor without reading it back (no host
+        sync).  The caller vouches that cu[0] = 0, cu is nondecreasing and
+        cu[-1] == total, as the reference's varlen callers do."""
+        if cu_dev.dtype != torch.int32 or cu_dev.dim() != 1 or cu_dev.numel() < 2 or cu_dev.device.type != "cuda":
+            raise ValueError("cu_seqlens must be a 1-D int32 cuda tensor with at least 2 entries")
+        obj = cls.__new__(cls)
+        obj.cu = None
+        obj.dev = cu_dev.contiguous()
+        obj._nseg, obj._total = cu_dev.numel() - 1, int(total)
+        return obj
 
     @property
     def nseg(self):
-        return len(self.cu) - 1
+        return self._nseg
 
     @property
     def total(self):
-        return self.cu[-1]
+        return self._total
 
     @property
     def max_len(self):

@@ -1,0 +1,364 @@
+"""SD3.5-Medium MMDiT on the ditk HIP kernels, packed over variable resolutions.
+
+Mirrors the reference's packed forward (workers/ditserve/models/sd35_batch.py:584-736):
+
+  forward_packed_sd35(torch_mod, transformer, latents_list, timesteps_list,
+                      encoder_hidden_states_list, pooled_projections_list) -> (outputs, meta)
+
+Image tokens of all requests are packed into one [sum N_m, D] buffer and text
+tokens into one [sum L_m, D] buffer; every projection, norm and FFN runs once
+over the packed rows, modulation is gathered per token by segment, and joint
+attention runs as one varlen flash launch over the joint layout (each segment's
+image tokens followed by its text tokens, cu_joint[m] = cu_img[m] + cu_txt[m],
+sd35_batch.py:230-317).  Each request's output is bitwise equal to its solo run.
+
+Block (sd35_batch.py:647-708), per JointTransformerBlock:
+  AdaLN-Zero (6 chunks, 9 with dual attention) on image and text, or
+  AdaLN-Continuous (scale, shift) on text for the last (context_pre_only) block;
+  joint attention with per-head QK RMSNorm; dual image-only attention (first
+  blocks); gated residuals; GELU-tanh FFNs on image and text.
+"""
+import dataclasses
+
+import torch
+
+from . import ops
+from .ops import Segments
+from .packing import joint_layout
+from .profiling import NULL as _NULL_PROFILER
+
+_BF16 = torch.bfloat16
+
+
+@dataclasses.dataclass(frozen=True)
+class SD35Config:
+    dim: int = 1536
+    heads: int = 24
+    head_dim: int = 64
+    layers: int = 24
+    dual_layers: tuple = tuple(range(13))
+    in_ch: int = 16
+    out_ch: int = 16
+    patch: int = 2
+    text_dim: int = 4096
+    pooled_dim: int = 2048
+    ffn: int = 6144
+    freq_dim: int = 256
+    eps: float = 1e-6
+    pos_max: int = 384
+    base_size: int = 64
+
+    def oracle_dict(self):
+        return dict(dim=self.dim, heads=self.heads, layers=self.layers, dual_layers=self.dual_layers,
+                    eps=self.eps, patch=self.patch, out_ch=self.out_ch, pos_max=self.pos_max,
+                    base_size=self.base_size)
+
+
+SD35_MEDIUM = SD35Config()
+
+
+def state_dict_shapes(cfg):
+    """diffusers SD3Transformer2DModel parameter names and shapes."""
+    D, F, P = cfg.dim, cfg.ffn, cfg.patch
+    s = {
+        "pos_embed.proj.weight": (D, cfg.in_ch, P, P), "pos_embed.proj.bias": (D,),
+        "time_text_embed.timestep_embedder.linear_1.weight": (D, cfg.freq_dim),
+        "time_text_embed.timestep_embedder.linear_1.bias": (D,),
+        "time_text_embed.timestep_embedder.linear_2.weight": (D, D),
+        "time_text_embed.timestep_embedder.linear_2.bias": (D,),
+        "time_text_embed.text_embedder.linear_1.weight": (D, cfg.pooled_dim),
+        "time_text_embed.text_embedder.linear_1.bias": (D,),
+        "time_text_embed.text_embedder.linear_2.weight": (D, D),
+        "time_text_embed.text_embedder.linear_2.bias": (D,),
+        "context_embedder.weight": (D, cfg.text_dim), "context_embedder.bias": (D,),
+        "norm_out.linear.weight": (2 * D, D), "norm_out.linear.bias": (2 * D,),
+        "proj_out.weight": (P * P * cfg.out_ch, D), "proj_out.bias": (P * P * cfg.out_ch,),
+    }
+    for i in range(cfg.layers):
+        b = f"transformer_blocks.{i}"
+        last, dual = i == cfg.layers - 1, i in cfg.dual_layers
+        s[f"{b}.norm1.linear.weight"] = ((9 if dual else 6) * D, D)
+        s[f"{b}.norm1.linear.bias"] = ((9 if dual else 6) * D,)
+        s[f"{b}.norm1_context.linear.weight"] = ((2 if last else 6) * D, D)
+        s[f"{b}.norm1_context.linear.bias"] = ((2 if last else 6) * D,)
+        names = ["to_q", "to_k", "to_v", "to_out.0", "add_q_proj", "add_k_proj", "add_v_proj"]
+        if not last:
+            names.append("to_add_out")
+        for n in names:
+            s[f"{b}.attn.{n}.weight"] = (D, D)
+            s[f"{b}.attn.{n}.bias"] = (D,)
+        for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+            s[f"{b}.attn.{n}.weight"] = (cfg.head_dim,)
+        if dual:
+            for n in ("to_q", "to_k", "to_v", "to_out.0"):
+                s[f"{b}.attn2.{n}.weight"] = (D, D)
+                s[f"{b}.attn2.{n}.bias"] = (D,)
+            for n in ("norm_q", "norm_k"):
+                s[f"{b}.attn2.{n}.weight"] = (cfg.head_dim,)
+        for ff in (["ff"] if last else ["ff", "ff_context"]):
+            s[f"{b}.{ff}.net.0.proj.weight"] = (F, D)
+            s[f"{b}.{ff}.net.0.proj.bias"] = (F,)
+            s[f"{b}.{ff}.net.2.weight"] = (D, F)
+            s[f"{b}.{ff}.net.2.bias"] = (D,)
+    return s
+
+
+def random_state_dict(cfg, seed=0, device="cpu", std=0.02):
+    """Synthetic random init rounded to bf16 values (fp32 tensors): weights and biases
+    N(0, std^2), RMSNorm weights N(1, std^2); deterministic per (seed, device)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    sd = {}
+    for name, shape in state_dict_shapes(cfg).items():
+        t = torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std
+        if ".norm_" in name:
+            t = t + 1.0
+        sd[name] = t.to(_BF16).float()
+    return sd
+
+
+def pos_embed_crop(cfg, hp, wp, device):
+    """Cropped 2D sin-cos position table [hp*wp, D] (fp32): centre crop of the
+    pos_max x pos_max grid with coordinates arange(n) * base_size / pos_max; the
+    first half of each vector encodes the column, the second half the row."""
+    top, left = (cfg.pos_max - hp) // 2, (cfg.pos_max - wp) // 2
+    scale = cfg.base_size / cfg.pos_max
+    rows = (torch.arange(top, top + hp, dtype=torch.float32) * scale).double()
+    cols = (torch.arange(left, left + wp, dtype=torch.float32) * scale).double()
+    half = cfg.dim // 2
+    omega = 1.0 / 10000 ** (torch.arange(half // 2, dtype=torch.float64) / (half / 2.0))
+
+    def enc(pos):
+        out = torch.outer(pos, omega)
+        return torch.cat([torch.sin(out), torch.cos(out)], dim=1)
+
+    ew = enc(cols).unsqueeze(0).expand(hp, wp, half)
+    eh = enc(rows).unsqueeze(1).expand(hp, wp, half)
+    return torch.cat([ew, eh], dim=-1).reshape(hp * wp, cfg.dim).float().to(device)
+
+
+class SD35Transformer:
+    """Device-resident SD3.5 MMDiT."""
+
+    def __init__(self, cfg, state_dict, device="cuda"):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        dev, D, H = self.device, cfg.dim, cfg.heads
+
+        def w(n):
+            t = state_dict[n]
+            return t.to(device=dev, dtype=_BF16).reshape(t.shape[0], -1).contiguous()
+
+        def f(n):
+            return state_dict[n].to(device=dev, dtype=torch.float32).contiguous()
+
+        def per_head(n):  # per-head RMSNorm weight repeated over heads -> [D]
+            return state_dict[n].to(device=dev, dtype=torch.float32).repeat(H).contiguous()
+
+        self.pe_w, self.pe_b = w("pos_embed.proj.weight"), f("pos_embed.proj.bias")
+        t = "time_text_embed"
+        self.te1 = (w(f"{t}.timestep_embedder.linear_1.weight"), f(f"{t}.timestep_embedder.linear_1.bias"))
+        self.te2 = (w(f"{t}.timestep_embedder.linear_2.weight"), f(f"{t}.timestep_embedder.linear_2.bias"))
+        self.pp1 = (w(f"{t}.text_embedder.linear_1.weight"), f(f"{t}.text_embedder.linear_1.bias"))
+        self.pp2 = (w(f"{t}.text_embedder.linear_2.weight"), f(f"{t}.text_embedder.linear_2.bias"))
+        self.ctx = (w("context_embedder.weight"), f("context_embedder.bias"))
+        self.norm_out = (w("norm_out.linear.weight"), f("norm_out.linear.bias"))
+        self.proj_out = (w("proj_out.weight"), f("proj_out.bias"))
+        self.blocks = []
+        for i in range(cfg.layers):
+            b = f"transformer_blocks.{i}"
+            a = f"{b}.attn"
+            last, dual = i == cfg.layers - 1, i in cfg.dual_layers
+            blk = {
+                "last": last, "dual": dual,
+                "n1": (w(f"{b}.norm1.linear.weight"), f(f"{b}.norm1.linear.bias")),
+                "n1c": (w(f"{b}.norm1_context.linear.weight"), f(f"{b}.norm1_context.linear.bias")),
+                "qkv": (torch.cat([w(f"{a}.to_q.weight"), w(f"{a}.to_k.weight"), w(f"{a}.to_v.weight")]),
+                        torch.cat([f(f"{a}.to_q.bias"), f(f"{a}.to_k.bias"), f(f"{a}.to_v.bias")])),
+                "qkv_t": (torch.cat([w(f"{a}.add_q_proj.weight"), w(f"{a}.add_k_proj.weight"),
+                                     w(f"{a}.add_v_proj.weight")]),
+                          torch.cat([f(f"{a}.add_q_proj.bias"), f(f"{a}.add_k_proj.bias"), f(f"{a}.add_v_proj.bias")])),
+                "nq": per_head(f"{a}.norm_q.weight"), "nk": per_head(f"{a}.norm_k.weight"),
+                "nqt": per_head(f"{a}.norm_added_q.weight"), "nkt": per_head(f"{a}.norm_added_k.weight"),
+                "out": (w(f"{a}.to_out.0.weight"), f(f"{a}.to_out.0.bias")),
+                "ff1": (w(f"{b}.ff.net.0.proj.weight"), f(f"{b}.ff.net.0.proj.bias")),
+                "ff2": (w(f"{b}.ff.net.2.weight"), f(f"{b}.ff.net.2.bias")),
+            }
+            if not last:
+                blk["out_t"] = (w(f"{a}.to_add_out.weight"), f(f"{a}.to_add_out.bias"))
+                blk["ffc1"] = (w(f"{b}.ff_context.net.0.proj.weight"), f(f"{b}.ff_context.net.0.proj.bias"))
+                blk["ffc2"] = (w(f"{b}.ff_context.net.2.weight"), f(f"{b}.ff_context.net.2.bias"))
+            if dual:
+                a2 = f"{b}.attn2"
+                blk["qkv2"] = (torch.cat([w(f"{a2}.to_q.weight"), w(f"{a2}.to_k.weight"), w(f"{a2}.to_v.weight")]),
+                               torch.cat([f(f"{a2}.to_q.bias"), f(f"{a2}.to_k.bias"), f(f"{a2}.to_v.bias")]))
+                blk["nq2"], blk["nk2"] = per_head(f"{a2}.norm_q.weight"), per_head(f"{a2}.norm_k.weight")
+                blk["out2"] = (w(f"{a2}.to_out.0.weight"), f(f"{a2}.to_out.0.bias"))
+            self.blocks.append(blk)
+        self._pos_cache = {}
+        self.profiler = _NULL_PROFILER
+
+    @classmethod
+    def random(cls, cfg, seed=0, device="cuda"):
+        return cls(cfg, random_state_dict(cfg, seed, device), device)
+
+    def _pos(self, hp, wp):
+        key = (hp, wp)
+        if key not in self._pos_cache:
+            self._pos_cache[key] = pos_embed_crop(self.cfg, hp, wp, self.device).to(_BF16)
+        return self._pos_cache[key]
+
+    # ------------------------------------------------------------------ pieces
+    def _attention(self, qkv, seg, wq, wk):
+        """Per-head QK RMSNorm (in place on the qkv buffer) + varlen flash over seg."""
+        D, H, Dh = self.cfg.dim, self.cfg.heads, self.cfg.head_dim
+        q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+        ops.qk_norm_rope_(q, k, wq, wk, Dh, self.cfg.eps, per_head=True)
+        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh)
+
+    def _block(self, i, h, c, st, seg_img, seg_txt, seg_joint):
+        cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
+        D, eps = cfg.dim, cfg.eps
+        with prof.region("adaln"):
+            emb = ops.linear(st, *blk["n1"], "f32")  # [M, 6D or 9D]
+            nh = ops.adaln(h, emb[:, 0:D], emb[:, D:2 * D], seg_img, eps=eps)
+            nh2 = ops.adaln(h, emb[:, 6 * D:7 * D], emb[:, 7 * D:8 * D], seg_img, eps=eps) if blk["dual"] else None
+            embc = ops.linear(st, *blk["n1c"], "f32")  # [M, 2D] (last) or [M, 6D]
+            if blk["last"]:  # AdaLN-Continuous: (scale, shift)
+                nc = ops.adaln(c, embc[:, D:2 * D], embc[:, 0:D], seg_txt, eps=eps)
+            else:
+                nc = ops.adaln(c, embc[:, 0:D], embc[:, D:2 * D], seg_txt, eps=eps)
+        with prof.region("gemm_qkv"):
+            qkv_i = ops.linear(nh, *blk["qkv"])
+            qkv_t = ops.linear(nc, *blk["qkv_t"])
+        with prof.region("attn_joint"):
+            D3 = 3 * D
+            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq"], blk["nk"], cfg.head_dim, eps, per_head=True)
+            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt"], blk["nkt"], cfg.head_dim, eps, per_head=True)
+            joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
+            a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], joint[:, 2 * D:D3], seg_joint, seg_joint,
+                                      cfg.heads, cfg.head_dim)
+            a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
+            a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
+            ops.joint_scatter(a, a_img, a_txt, seg_img, seg_txt)
+        with prof.region("gemm_out"):
+            h = ops.linear(a_img, *blk["out"], "gate_res", residual=h, gate=emb[:, 2 * D:3 * D], segments=seg_img)
+        if blk["dual"]:
+            with prof.region("attn_dual"):
+                qkv2 = ops.linear(nh2, *blk["qkv2"])
+                a2 = self._attention(qkv2, seg_img, blk["nq2"], blk["nk2"])
+                ops.linear(a2, *blk["out2"], "gate_res", residual=h, gate=emb[:, 8 * D:9 * D], segments=seg_img, out=h)
+        with prof.region("ffn"):
+            n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)
+            fx = ops.linear(n2, *blk["ff1"], "gelu")
+            ops.linear(fx, *blk["ff2"], "gate_res", residual=h, gate=emb[:, 5 * D:6 * D], segments=seg_img, out=h)
+            if blk["last"]:
+                return h, None
+            c = ops.linear(a_txt, *blk["out_t"], "gate_res", residual=c, gate=embc[:, 2 * D:3 * D], segments=seg_txt)
+            n2c = ops.adaln(c, embc[:, 3 * D:4 * D], embc[:, 4 * D:5 * D], seg_txt, eps=eps)
+            fc = ops.linear(n2c, *blk["ffc1"], "gelu")
+            ops.linear(fc, *blk["ffc2"], "gate_res", residual=c, gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c)
+        return h, c
+
+    # ------------------------------------------------------------------ forward
+    def forward_packed(self, latents, timesteps, texts, pooleds):
+        """latents: list of [C, H, W] (or [1, C, H, W]); timesteps: list of scalars;
+        texts: list of [L, text_dim]; pooleds: list of [pooled_dim].
+        Returns (list of fp32 [C, H, W], meta)."""
+        cfg, dev, D = self.cfg, self.device, self.cfg.dim
+        n = len(latents)
+        if n == 0:
+            raise ValueError("forward_packed requires at least one item")
+        if not (len(timesteps) == len(texts) == len(pooleds) == n):
+            raise ValueError("all input lists must have matching lengths")
+        P = cfg.patch
+        lats = [l.reshape(l.shape[-3:]) for l in latents]
+        hw = []
+        for l in lats:
+            if l.shape[0] != cfg.in_ch or l.shape[1] % P or l.shape[2] % P:
+                raise ValueError(f"latent {tuple(l.shape)} must be [{cfg.in_ch}, H, W] with H, W divisible by {P}")
+            hw.append((l.shape[1] // P, l.shape[2] // P))
+        img_counts = [a * b for a, b in hw]
+        txts = [t.reshape(-1, cfg.text_dim) for t in texts]
+        txt_counts = [t.shape[0] for t in txts]
+        lay = joint_layout(img_counts, txt_counts)
+        seg_img, seg_txt = Segments(lay["cu_img"], dev), Segments(lay["cu_txt"], dev)
+        seg_joint = Segments(lay["cu_joint"], dev)
+        # prelude: patch embed (+ cropped 2D sin-cos positions), context embedder, temb
+        h = torch.empty((seg_img.total, D), dtype=_BF16, device=dev)
+        for m, (l, (hp, wp)) in enumerate(zip(lats, hw)):
+            patches = ops.patchify(l.reshape(cfg.in_ch, 1, *l.shape[1:]).to(_BF16), (1, P, P))
+            rows = h[seg_img.cu[m]:seg_img.cu[m + 1]]
+            ops.linear(patches, self.pe_w, self.pe_b, "res", residual=self._pos(hp, wp), out=rows)
+        c = ops.linear(torch.cat([t.to(device=dev, dtype=_BF16) for t in txts]), *self.ctx)
+        t = torch.tensor([float(x) for x in timesteps], dtype=torch.float32, device=dev)
+        te = ops.linear(ops.linear(ops.timestep_embedding(t, cfg.freq_dim), *self.te1, "silu"), *self.te2)
+        pooled = torch.stack([p.reshape(-1) for p in pooleds]).to(device=dev, dtype=_BF16)
+        temb = ops.linear(ops.linear(pooled, *self.pp1, "silu"), *self.pp2, "res", residual=te)
+        st = ops.silu(temb)
+        for i in range(cfg.layers):
+            h, c = self._block(i, h, c, st, seg_img, seg_txt, seg_joint)
+        # epilogue: AdaLN-Continuous norm_out (scale, shift), proj_out, per-request unpatchify
+        embo = ops.linear(st, *self.norm_out, "f32")
+        x = ops.adaln(h, embo[:, D:2 * D], embo[:, 0:D], seg_img, eps=cfg.eps)
+        y = ops.linear(x, *self.proj_out)
+        outs = []
+        for m, (hp, wp) in enumerate(hw):
+            u = ops.unpatchify(y[seg_img.cu[m]:seg_img.cu[m + 1]], (1, hp, wp), (1, P, P), cfg.out_ch)
+            outs.append(u.reshape(cfg.out_ch, hp * P, wp * P))
+        meta = {
+            "sequence_packed": True,
+            "attention_backend": "ditk_flash_varlen",
+            "packed_segments": n,
+            "cu_seqlens_img": lay["cu_img"],
+            "cu_seqlens_txt": lay["cu_txt"],
+            "cu_seqlens_joint": lay["cu_joint"],
+            "packed_image_tokens": lay["cu_img"][-1],
+            "padded_image_tokens": n * max(img_counts),
+            "padding_saved_tokens": n * max(img_counts) - lay["cu_img"][-1],
+        }
+        return outs, meta
+
+    def forward(self, hidden_states, timestep, encoder_hidden_states, pooled_projections):
+        """Dense batch (e.g. the homogeneous CFG batch of workers/ditserve/models/sd35.py:956-1017):
+        hidden_states [B, C, H, W] -> [B, C, H, W] fp32."""
+        b = hidden_states.shape[0]
+        ts = timestep.reshape(-1).tolist() if torch.is_tensor(timestep) else list(timestep)
+        if len(ts) == 1:
+            ts = ts * b
+        outs, _ = self.forward_packed([hidden_states[i] for i in range(b)], ts,
+                                      [encoder_hidden_states[i] for i in range(b)],
+                                      [pooled_projections[i] for i in range(b)])
+        return torch.stack(outs)
+
+
+def forward_packed_sd35(torch_mod, transformer, latents_list, timesteps_list, encoder_hidden_states_list,
+                        pooled_projections_list):
+    """Signature of the reference's packed forward (sd35_batch.py:584-591); ``torch_mod``
+    is accepted for call compatibility and ``transformer`` is an SD35Transformer.
+    Latents are [1, C, h, w] each; returns ([1, C, h, w] outputs, meta)."""
+    for lat in latents_list:
+        if lat.ndim != 4 or lat.shape[0] != 1:
+            raise ValueError("each latent in latents_list must have shape [1, C, H_lat, W_lat]")
+    for enc in encoder_hidden_states_list:
+        if enc.ndim != 3 or enc.shape[0] != 1:
+            raise ValueError("each encoder_hidden_states item must have shape [1, L, D_ctx]")
+    outs, meta = transformer.forward_packed(latents_list, [float(t.reshape(-1)[0]) if torch.is_tensor(t) else float(t)
+                                                           for t in timesteps_list],
+                                            encoder_hidden_states_list, pooled_projections_list)
+    return [o.unsqueeze(0) for o in outs], meta
+
+
+def step_flops(cfg, img_counts, txt_counts):
+    """Algorithmic FLOPs of the transformer blocks for one packed forward."""
+    D, F = cfg.dim, cfg.ffn
+    total = 0
+    for i in range(cfg.layers):
+        last, dual = i == cfg.layers - 1, i in cfg.dual_layers
+        for n, l in zip(img_counts, txt_counts):
+            total += 2 * n * D * 3 * D + 2 * l * D * 3 * D          # QKV image + text
+            total += 4 * (n + l) ** 2 * D                           # joint attention
+            total += 2 * n * D * D + (0 if last else 2 * l * D * D)  # to_out / to_add_out
+            total += 4 * n * D * F + (0 if last else 4 * l * D * F)  # FFNs
+            if dual:
+                total += 2 * n * D * 3 * D + 4 * n * n * D + 2 * n * D * D
+    return total

@@ -121,9 +121,10 @@ def pos_embed_crop(cfg, hp, wp, device):
     pos_max x pos_max grid with coordinates arange(n) * base_size / pos_max; the
     first half of each vector encodes the column, the second half the row."""
     top, left = (cfg.pos_max - hp) // 2, (cfg.pos_max - wp) // 2
-    scale = cfg.base_size / cfg.pos_max
-    rows = (torch.arange(top, top + hp, dtype=torch.float32) * scale).double()
-    cols = (torch.arange(left, left + wp, dtype=torch.float32) * scale).double()
+    # fp32 coordinates i / (pos_max / base_size), as the table's grid is built
+    coords = torch.arange(cfg.pos_max, dtype=torch.float32) / (cfg.pos_max / cfg.base_size)
+    rows = coords[top:top + hp].double()
+    cols = coords[left:left + wp].double()
     half = cfg.dim // 2
     omega = 1.0 / 10000 ** (torch.arange(half // 2, dtype=torch.float64) / (half / 2.0))
 

@@ -27,6 +27,13 @@ TIMESTEP = 999.0
 GUIDANCE = 5.0
 EULER_DT = -1.0 / 50.0
 CALIB_BYTES = 256 << 20
+# A100-PCIe-40GB, fp16, same workload: 3964.62 ms per step (the reference's published figure)
+REFERENCE_STEPS_PER_S = 1000.0 / 3964.62
+# HBM traffic of one self-attention launch, from two rocprofv3 --pmc passes over this
+# bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that counter's
+# reading for the CALIB_BYTES copy: FETCH 917467.5 KiB x 1.9997, WRITE 196581.8 KiB x 1.0000
+# (profiles/wan21_480p_cfg2_step_traffic.md).  Re-measure after kernel changes.
+ATTN_SELF_TRAFFIC_BYTES = (917467.5 * 1.9997 + 196581.8 * 1.0000) * 1024
 
 
 def parse_args():
@@ -145,7 +152,7 @@ def main():
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": (1000.0 / ms) / REFERENCE_STEPS_PER_S,
         "dtype": "bf16",
         "data": "synthetic: random-init weights N(0,0.02^2), latent/text N(0,1)",
         "config": {"workload": "Wan2.1-T2V-1.3B-architecture denoise step, latent 16x21x60x104 (480x832x81f), "
@@ -161,12 +168,14 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": attn_tflops / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": ATTN_SELF_TRAFFIC_BYTES,
+            "traffic_unit": "bytes/launch",
+            "algorithmic_bytes": 4.0 * 2 * seq * cfg.dim * 2,
             "avg_launch_ms": attn["avg_ms"],
             "launches": attn["count"],
             "flops_per_launch": attn_flops,
         },
-        "reference_a100_steps_per_s": 1000.0 / 3964.62,
+        "reference_a100_steps_per_s": REFERENCE_STEPS_PER_S,
     }
     if args.breakdown:
         out["breakdown_ms_per_step"] = {k: v["total_ms"] / args.steps for k, v in regions.items()}

@@ -48,6 +48,25 @@ class SD35Config:
     pos_max: int = 384
     base_size: int = 64
 
+    @classmethod
+    def from_diffusers(cls, config):
+        """From a diffusers SD3Transformer2DModel config (a mapping or an object with
+        attributes)."""
+        get = config.get if isinstance(config, dict) else (lambda k, d=None: getattr(config, k, d))
+        if get("qk_norm") != "rms_norm":
+            raise ValueError("SD3.5 blocks here need qk_norm='rms_norm'")
+        heads, hd = int(get("num_attention_heads")), int(get("attention_head_dim"))
+        dim = heads * hd
+        if int(get("caption_projection_dim")) != dim:
+            raise ValueError("caption_projection_dim must equal the hidden size")
+        patch = int(get("patch_size"))
+        return cls(dim=dim, heads=heads, head_dim=hd, layers=int(get("num_layers")),
+                   dual_layers=tuple(get("dual_attention_layers") or ()), in_ch=int(get("in_channels")),
+                   out_ch=int(get("out_channels") or get("in_channels")), patch=patch,
+                   text_dim=int(get("joint_attention_dim")), pooled_dim=int(get("pooled_projection_dim")),
+                   ffn=4 * dim, pos_max=int(get("pos_embed_max_size")),
+                   base_size=int(get("sample_size")) // patch)
+
     def oracle_dict(self):
         return dict(dim=self.dim, heads=self.heads, layers=self.layers, dual_layers=self.dual_layers,
                     eps=self.eps, patch=self.patch, out_ch=self.out_ch, pos_max=self.pos_max,

@@ -55,6 +55,22 @@ class WanConfig:
     def as_dict(self):
         return dataclasses.asdict(self)
 
+    @classmethod
+    def from_diffusers(cls, config, text_len=512):
+        """From a diffusers WanTransformer3DModel config (a mapping or an object with
+        attributes): the keys its constructor takes.  ``text_len`` is the
+        pipeline's padded prompt length, not part of that config."""
+        get = config.get if isinstance(config, dict) else (lambda k, d=None: getattr(config, k, d))
+        if get("added_kv_proj_dim") is not None or get("image_dim") is not None:
+            raise ValueError("only text-to-video Wan transformers (no image conditioning) are supported")
+        if get("qk_norm", "rms_norm_across_heads") != "rms_norm_across_heads" or not get("cross_attn_norm", True):
+            raise ValueError("Wan blocks need qk_norm='rms_norm_across_heads' and cross_attn_norm=True")
+        heads, hd = int(get("num_attention_heads")), int(get("attention_head_dim"))
+        return cls(dim=heads * hd, heads=heads, head_dim=hd, ffn=int(get("ffn_dim")), layers=int(get("num_layers")),
+                   in_ch=int(get("in_channels")), out_ch=int(get("out_channels")), text_dim=int(get("text_dim")),
+                   text_len=text_len, freq_dim=int(get("freq_dim")), patch=tuple(get("patch_size")),
+                   eps=float(get("eps")), rope_max_seq_len=int(get("rope_max_seq_len")))
+
 
 WAN21_T2V_1_3B = WanConfig()
 WAN22_TI2V_5B = WanConfig(dim=3072, heads=24, ffn=14336, in_ch=48, out_ch=48)

@@ -10,8 +10,10 @@
 // at the 64-aligned column pk[m] = 64 * sum_{m'<m} ceil(len_k[m'] / 64) and the
 // padding columns are zero.  ditk_transpose_v produces it.
 //
-// Per workgroup: 4 waves x 64 queries of one (segment, head); K/Vt tiles of 64
-// keys are staged through double-buffered LDS.  Each wave computes
+// Per workgroup: NW waves x QB*32 queries of one (segment, head) (defaults 8 x 32:
+// two waves per SIMD, so one wave's softmax overlaps the other's MFMAs); K/Vt
+// tiles of 64 keys are staged through LDS by direct global->LDS DMA (three K
+// stages, two Vt stages).  Each wave computes
 //   S^T = K Q^T        (A = K rows from LDS, B = Q held in registers)
 //   P^T = exp2(S^T * scale*log2e - m)   (online softmax, fp32)
 //   O^T += Vt P^T      (A = Vt rows from LDS, B = P^T straight from registers)
@@ -19,7 +21,9 @@
 // (kperm) so that the S^T accumulator registers of each lane are exactly the
 // B-operand layout of the second MFMA: no shuffles between the two products.
 // Each lane owns one query of each 32-query tile, so softmax statistics are
-// per-lane scalars combined across the two half-waves with one shuffle.
+// per-lane scalars combined across the two half-waves with one shuffle.  The
+// running max is raised lazily (see rescale_tile), so the common path per score
+// is one fma, one exp2, half a bf16 pack and one add.
 //
 // Query tiles start at each segment's first query and the key loop starts at
 // each segment's first key, so results are independent of packing: a request
@@ -30,21 +34,16 @@ namespace {
 
 constexpr int BN = 64;   // keys per iteration
 #ifndef ATTN_NW
-#define ATTN_NW 8        // waves per workgroup (32 queries each)
+#define ATTN_NW 8        // waves per workgroup
 #endif
-#ifndef ATTN_MINB
-#define ATTN_MINB 1      // workgroups per CU the register budget must allow
+#ifndef ATTN_QB
+#define ATTN_QB 1        // 32-query blocks per wave
 #endif
 #ifndef ATTN_SCHED
-#define ATTN_SCHED 0     // interleave MFMA / VALU / LDS reads with sched_group_barrier
-#endif
-#ifndef ATTN_FENCE
-#define ATTN_FENCE 1     // keep those reads ahead of the MFMAs (scheduling fence)
-#endif
-#ifndef ATTN_PREFETCH
-#define ATTN_PREFETCH 1  // issue a phase's LDS operand reads before its MFMAs
+#define ATTN_SCHED 0     // steady loop: 1 = fenced MFMA/VALU interleave, 0 = compiler order
 #endif
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
+constexpr float kRescaleSum = 256.0f;  // 2^kLazy: a lane's row sum above it triggers a rescale
 
 // S^T row m of a 32-key MFMA tile holds key kperm(m): with the D layout
 // row = (v/4)*8 + (lane/32)*4 + v%4, this puts key (v/8)*16 + (lane/32)*8 + v%8
@@ -93,24 +92,27 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 // 16 consecutive lanes reading one chunk of 16 different rows hit 16 distinct
 // 16-byte bank groups; each lane's read address is one of 4 per-lane bases
 // plus a compile-time offset.
-// Pipeline per iteration kt (steady state), per wave:
-//   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) = exp2(S(kt) - m) on VALU
-//   B: O += Vt(kt) P(kt) on MFMA       ||  row max of S(kt+1) on VALU
-// K runs one tile ahead of V through two LDS stages each.
-template <int HD, int NW>
-__global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
+// Per workgroup: NW waves x QB*32 queries of one (segment, head); per wave and
+// 64-key tile kt (steady state):
+//   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) = exp2(S(kt) c - m) on VALU
+//   B: O += Vt(kt) P(kt) on MFMA
+// Each K / Vt fragment read from LDS feeds QB MFMAs (one per 32-query block).
+// K(kt) sits in LDS stage kt % 3 (kept resident for the rescale path while
+// K(kt+2) streams in), Vt(kt) in stage kt % 2.
+template <int HD, int NW, int QB>
+__global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
     float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
-  constexpr int BM = NW * 32;            // queries per workgroup (32 per wave)
+  constexpr int BM = NW * QB * 32;       // queries per workgroup
   constexpr int NC = HD / 16;            // 16-wide k chunks of the head dim
   constexpr int KCH = HD / 8;            // 16-byte chunks per K row
   constexpr int DT = HD / 32;            // 32-row d tiles of O^T
   constexpr int K_LOADS = BN * KCH / 64 / NW;   // 64-slot DMA groups per wave
   constexpr int V_LOADS = HD * 8 / 64 / NW;
   static_assert(K_LOADS >= 1 && V_LOADS >= 1 && (BN * KCH / 64) % NW == 0, "tile too small for the workgroup");
-  __shared__ u32x4_t Ks[2][BN * KCH];
+  __shared__ u32x4_t Ks[3][BN * KCH];
   __shared__ u32x4_t Vs[2][HD * 8];
 
   // XCD-aware order: hardware deals workgroup ids round-robin over 8 XCDs, so
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
   const int l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int q_end = cu_q[seg + 1];
-  const int qrow = cu_q[seg] + t * BM + wave * 32 + l32;
+  const int qrow0 = cu_q[seg] + t * BM + wave * (QB * 32) + l32;  // query of block qb: qrow0 + 32 * qb
   const int k_beg = cu_k[seg], k_len = cu_k[seg + 1] - k_beg;
   const int pk = padded_key_start(cu_k, seg);
 
@@ -137,21 +139,31 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
   const bf16_t* Kh = Kp + (int64_t)head * HD + (int64_t)k_beg * ldk;
   const bf16_t* Vh = Vt + (int64_t)head * vt_hs + pk;
 
-  // ---- Q fragments (B operand of S^T): lane -> query l32, k-slot hh*8..+8
-  bf16x8_t qf[NC];
+  // ---- Q fragments (B operand of S^T): lane -> query l32 of block qb, k-slot hh*8..+8
+  bf16x8_t qf[QB][NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    u32x4_t v = u32x4_t{0, 0, 0, 0};
-    if (qrow < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
-    qf[c] = __builtin_bit_cast(bf16x8_t, v);
-  }
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      u32x4_t v = u32x4_t{0, 0, 0, 0};
+      const int qrow = qrow0 + 32 * qb;
+      if (qrow < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
+      qf[qb][c] = __builtin_bit_cast(bf16x8_t, v);
+    }
 
-  f32x16_t o[DT];
+  f32x16_t o[QB][DT];
 #pragma unroll
-  for (int d = 0; d < DT; ++d)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) o[d][v] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[qb][d][v] = 0.f;
+  float m_run[QB], l_run[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+  }
 
   // ---- DMA (global -> LDS, 16 B per lane).  Instruction i of wave w fills
   // slots [g*64, g*64 + 64), g = i*NW + w: rows 8*(g%(rows/8)) .. +8 of chunk
@@ -161,27 +173,40 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
   const int lrow = lane >> 3;
   const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;        // chunk offset, k even
   const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;  // chunk offset, k odd
+  // Per-lane element offsets of each DMA instruction from the tile's uniform base
+  // (32-bit: the host bounds 64 rows of K and HD rows of Vt below 2^31 elements).
+  uint32_t k_off[K_LOADS], k_col[K_LOADS], v_off[V_LOADS];
+  int k_row[K_LOADS];
+#pragma unroll
+  for (int i = 0; i < K_LOADS; ++i) {
+    const int g = i * NW + wave_u;
+    const int grp = g / (BN / 8), r8 = g % (BN / 8);
+    k_row[i] = r8 * 8 + lrow;
+    k_col[i] = (uint32_t)(grp * 64 + ((r8 & 1) ? lsw1 : lsw0));
+    k_off[i] = (uint32_t)k_row[i] * (uint32_t)ldk + k_col[i];
+  }
+#pragma unroll
+  for (int i = 0; i < V_LOADS; ++i) {
+    const int g = i * NW + wave_u;
+    v_off[i] = (uint32_t)(g * 8 + lrow) * (uint32_t)vt_ld + (uint32_t)((g & 1) ? lsw1 : lsw0);
+  }
   auto issue_k = [&](int kt, int s) {
     const int kb = kt * BN;
-    const bool full = kb + BN <= k_len;
+    const bf16_t* base = Kh + (int64_t)kb * ldk;
+    if (kb + BN <= k_len) {
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int g = i * NW + wave_u;
-      const int grp = g / (BN / 8), r8 = g % (BN / 8);
-      int row = r8 * 8 + lrow;
-      if (!full) row = min(row, k_len - kb - 1);
-      const int cho = grp * 64 + ((r8 & 1) ? lsw1 : lsw0);
-      lds_dma16(Kh + (int64_t)(kb + row) * ldk + cho, &Ks[s][g * 64]);
+      for (int i = 0; i < K_LOADS; ++i) lds_dma16(base + k_off[i], &Ks[s][(i * NW + wave_u) * 64]);
+    } else {
+      const int last = k_len - kb - 1;
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i)
+        lds_dma16(base + (uint32_t)min(k_row[i], last) * (uint32_t)ldk + k_col[i], &Ks[s][(i * NW + wave_u) * 64]);
     }
   };
   auto issue_v = [&](int kt, int s) {
-    const int kb = kt * BN;
+    const bf16_t* base = Vh + kt * BN;
 #pragma unroll
-    for (int i = 0; i < V_LOADS; ++i) {
-      const int g = i * NW + wave_u;
-      const int d = g * 8 + lrow;
-      lds_dma16(Vh + (int64_t)d * vt_ld + kb + ((g & 1) ? lsw1 : lsw0), &Vs[s][g * 64]);
-    }
+    for (int i = 0; i < V_LOADS; ++i) lds_dma16(base + v_off[i], &Vs[s][(i * NW + wave_u) * 64]);
   };
 
   // per-lane read bases (slot units): K row kperm(l32), chunk (c%4)*2 + hh;
@@ -196,64 +221,44 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
       vbase[i] = l32 * 8 + ((i * 2 + hh) ^ vg);
     }
   }
-  auto compute_s = [&](int s, f32x16_t (&sacc)[2]) {
+  auto k_frag = [&](int s, int c, int kk) {
+    return __builtin_bit_cast(bf16x8_t, Ks[s][kbase[c & 3] + (c >> 2) * BN * 8 + kk * 256]);
+  };
+  auto v_frag = [&](int s, int g, int d) { return __builtin_bit_cast(bf16x8_t, Vs[s][vbase[g] + d * 256]); };
+
+  // S^T = K(stage s) Q^T from scratch, one K chunk in flight (prologue and the
+  // rare rescale path; the steady loop interleaves its own S product)
+  auto compute_s = [&](int s, f32x16_t (&sacc)[QB][2]) {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sacc[kk][v] = 0.f;
-#if ATTN_PREFETCH
-    bf16x8_t kf[NC][2];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        kf[c][kk] = __builtin_bit_cast(bf16x8_t, Ks[s][kbase[c & 3] + (c >> 2) * BN * 8 + kk * 256]);
-#if ATTN_FENCE
-    __builtin_amdgcn_sched_barrier(0);
-#endif
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
-        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c][kk], qf[c], sacc[kk], 0, 0, 0);
-#else
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+        for (int v = 0; v < 16; ++v) sacc[qb][kk][v] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        bf16x8_t kf = __builtin_bit_cast(bf16x8_t, Ks[s][kbase[c & 3] + (c >> 2) * BN * 8 + kk * 256]);
-        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], sacc[kk], 0, 0, 0);
+        const bf16x8_t kf = k_frag(s, c, kk);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          sacc[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][c], sacc[qb][kk], 0, 0, 0);
       }
-#endif
+      __builtin_amdgcn_sched_barrier(0);  // bounded register use: one chunk in flight
+    }
   };
+  // row max of S^T for this lane's query of block qb, scaled to log2 units
   auto row_max = [&](const f32x16_t (&sacc)[2]) {
-    float a = fmaxf(sacc[0][0], sacc[0][1]), c = fmaxf(sacc[1][0], sacc[1][1]);
+    float a = fmaxf(sacc[0][0], sacc[1][0]);
 #pragma unroll
-    for (int v = 2; v < 16; v += 2) {
-      a = fmaxf(a, fmaxf(sacc[0][v], sacc[0][v + 1]));
-      c = fmaxf(c, fmaxf(sacc[1][v], sacc[1][v + 1]));
-    }
-    const float mx = fmaxf(a, c);
-    return fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    for (int v = 1; v < 16; ++v) a = fmaxf(a, fmaxf(sacc[0][v], sacc[1][v]));
+    return fmaxf(a, __shfl_xor(a, 32, 64)) * scale_log2;
   };
-  // lazy rescale: raise the reference max only when a query's tile max exceeds
-  // it by more than 2^kLazy (wave vote); P stays <= 2^kLazy in between.
-  auto maybe_rescale = [&](float mt) {
-    if (__any(mt > m_run + kLazy)) {
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < DT; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
-    }
-  };
-  // P = exp2(S*c - m) as bf16 B-operand fragments; returns the fp32 row sum
-  // over keys < valid (key of register v in key tile kk: kk*32 + (v/8)*16 + hh*8 + v%8).
-  auto softmax_p = [&](const f32x16_t (&sacc)[2], uint32_t (&pf)[2][2][4], int valid) {
-    const float neg_m = -m_run;
+  // P = exp2(S*c - m) as bf16 B-operand fragments for one query block; returns
+  // the fp32 row sum over keys < valid (key of register v in key tile kk:
+  // kk*32 + (v/8)*16 + hh*8 + v%8).
+  auto softmax_p = [&](const f32x16_t (&sacc)[2], uint32_t (&pf)[2][2][4], float m, int valid) {
+    const float neg_m = -m;
     float rs = 0.f;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -264,51 +269,72 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
           const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e], scale_log2, neg_m));
           const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e + 1], scale_log2, neg_m));
           pf[kk][j][e] = pack_bf2(p0, p1);
-          if (valid >= BN) {
-            rs += p0 + p1;
-          } else {
-            const int key = kk * 32 + j * 16 + hh * 8 + 2 * e;
-            rs += (key < valid ? p0 : 0.f) + (key + 1 < valid ? p1 : 0.f);
-          }
+          const int key = kk * 32 + j * 16 + hh * 8 + 2 * e;
+          rs += (key < valid ? p0 : 0.f) + (key + 1 < valid ? p1 : 0.f);
         }
     return rs;
   };
-  auto pv = [&](int s, const uint32_t (&pf)[2][2][4]) {
-#if ATTN_PREFETCH
-    bf16x8_t vf[2][2][DT];
+  // Lazy rescale.  P(kt) is first computed against the running reference m;
+  // while every score stays below m + kLazy, each P <= 2^kLazy and this lane's
+  // row sum over its 32 keys stays <= 32 * 2^kLazy.  A sum above 2^kLazy (or a
+  // non-finite one) therefore flags every tile that might break that bound
+  // (plus a few that do not): then, rarely, S(kt) is recomputed from K(kt),
+  // still resident in its LDS stage, m is raised to the tile's max, O and l are
+  // rescaled and P(kt) is recomputed, for all query blocks of the wave.
+  auto needs_rescale = [&](const float (&rs)[QB]) {
+    bool r = false;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int qb = 0; qb < QB; ++qb) r |= !(rs[qb] <= kRescaleSum);
+    return __any(r);
+  };
+  auto rescale_tile = [&](int kstage, uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
+    f32x16_t sr[QB][2];
+    compute_s(kstage, sr);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int qb = 0; qb < QB; ++qb) {
+      const float m_new = fmaxf(m_run[qb], row_max(sr[qb]));
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+      m_run[qb] = m_new;
+      l_run[qb] *= alpha;
 #pragma unroll
-        for (int d = 0; d < DT; ++d)
-          vf[kk][j][d] = __builtin_bit_cast(bf16x8_t, Vs[s][vbase[kk * 2 + j] + d * 256]);
-#if ATTN_FENCE
-    __builtin_amdgcn_sched_barrier(0);
-#endif
-#endif
+      for (int d = 0; d < DT; ++d)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+        for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
+      rs[qb] = softmax_p(sr[qb], pf[qb], m_run[qb], valid);
+    }
+  };
+  auto pv = [&](int s, const uint32_t (&pf)[QB][2][2][4]) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int g = 0; g < 4; ++g)  // g = kk * 2 + j
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-#if ATTN_PREFETCH
-          const bf16x8_t v8 = vf[kk][j][d];
-#else
-          const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, Vs[s][vbase[kk * 2 + j] + d * 256]);
-#endif
-          u32x4_t p4 = u32x4_t{pf[kk][j][0], pf[kk][j][1], pf[kk][j][2], pf[kk][j][3]};
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v8, __builtin_bit_cast(bf16x8_t, p4), o[d], 0, 0, 0);
+      for (int d = 0; d < DT; ++d) {
+        const bf16x8_t v8 = v_frag(s, g, d);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const uint32_t* p = pf[qb][g >> 1][g & 1];
+          const u32x4_t p4 = u32x4_t{p[0], p[1], p[2], p[3]};
+          o[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v8, __builtin_bit_cast(bf16x8_t, p4), o[qb][d], 0, 0, 0);
         }
+      }
+  };
+  // keep packed P in registers where it is made: otherwise the packing sinks
+  // below the rescale branch and the fp32 values stay live across it
+  auto pin = [&](uint32_t (&pf)[QB][2][2][4]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(pf[qb][kk][j][e]));
   };
 
   // Keys past the segment end are clamped duplicates of its last key: they
   // cannot raise a row max, their Vt columns are zero, and only the final
   // tile's row sum has to skip them.
   const int nkt = (k_len + BN - 1) / BN;
-  f32x16_t s_next[2];
-  float mt_next = -INFINITY;
+  f32x16_t s_next[QB][2];
   if (nkt > 0) {
     issue_k(0, 0);
     dma_wait();
@@ -316,68 +342,153 @@ __global__ __launch_bounds__(NW * 64, ATTN_MINB) void flash_fwd_kernel(
     compute_s(0, s_next);
     if (nkt > 1) issue_k(1, 1);
     issue_v(0, 0);
-    mt_next = row_max(s_next);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) m_run[qb] = row_max(s_next[qb]);  // exact max of the first tile
     dma_wait();
     __syncthreads();
   }
 
-  // steady state: every tile but the last (all full)
-  for (int kt = 0; kt + 1 < nkt; ++kt) {
-    f32x16_t s_cur[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) s_cur[kk] = s_next[kk];
-    maybe_rescale(mt_next);
-    const int sk = kt & 1;
-    if (kt + 2 < nkt) issue_k(kt + 2, sk);
-    issue_v(kt + 1, sk ^ 1);
-    uint32_t pf[2][2][4];
-    // phase A: S(kt+1) on MFMA || P(kt) on VALU;  phase B: O += Vt P || max S(kt+1)
-    l_run += softmax_p(s_cur, pf, BN);
-    compute_s(sk ^ 1, s_next);
-    pv(sk, pf);
-    mt_next = row_max(s_next);
+  // Steady-state iteration for tile kt (never the last tile, so all 64 keys are
+  // valid).  ATTN_SCHED 1: scheduling-fenced groups, K(kt+1) chunks read four
+  // ahead, each group = the MFMAs of one K chunk for all query blocks and
+  // 16*QB/NC score pairs of P(kt); Vt(kt) reads two groups ahead of the PV MFMAs.
+  // ATTN_SCHED 0: P(kt), then S(kt+1), then PV, scheduled by the compiler.
+  auto steady = [&](int kt, const f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2]) {
+    const int kcur = kt % 3, knxt = (kt + 1) % 3, vcur = kt & 1;
+    if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % 3);
+    issue_v(kt + 1, vcur ^ 1);
+    uint32_t pf[QB][2][2][4];
+    float rs[QB];
 #if ATTN_SCHED
 #pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // ds_read (K)
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // mfma (S)
-      __builtin_amdgcn_sched_group_barrier(0x002, 112 / (2 * NC), 0);  // valu (softmax)
-    }
+    for (int qb = 0; qb < QB; ++qb) {
+      rs[qb] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4 * DT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // ds_read (Vt)
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // mfma (PV)
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // valu (row max)
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s_nxt[qb][kk][v] = 0.f;
     }
+    bf16x8_t kf[NC][2];
+    auto read_k = [&](int c) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) kf[c][kk] = k_frag(knxt, c, kk);
+    };
+    constexpr int KAHEAD = NC < 4 ? NC : 4;
+#pragma unroll
+    for (int c = 0; c < KAHEAD; ++c) read_k(c);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int PAIRS = 16 * QB / NC;  // score pairs of P(kt) per group
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (c + KAHEAD < NC) read_k(c + KAHEAD);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c][kk], qf[qb][c], s_nxt[qb][kk], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < PAIRS; ++i) {
+        const int pi = c * PAIRS + i, qb = pi >> 4, kk = (pi >> 3) & 1, j = (pi >> 2) & 1, e = pi & 3;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+        pf[qb][kk][j][e] = pack_bf2(p0, p1);
+        rs[qb] += p0 + p1;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pin(pf);
+    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
+    bf16x8_t vf[4][DT];
+    auto read_v = [&](int g) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d) vf[g][d] = v_frag(vcur, g, d);
+    };
+    read_v(0);
+    read_v(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (g + 2 < 4) read_v(g + 2);
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const uint32_t* p = pf[qb][g >> 1][g & 1];
+          const u32x4_t p4 = u32x4_t{p[0], p[1], p[2], p[3]};
+          o[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[g][d], __builtin_bit_cast(bf16x8_t, p4), o[qb][d], 0, 0, 0);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#else
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s_cur[qb], pf[qb], m_run[qb], BN);
+    pin(pf);
+    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
+    compute_s(knxt, s_nxt);
+    pv(vcur, pf);
 #endif
     dma_wait();
     __syncthreads();
-  }
-
-  // last tile
-  if (nkt > 0) {
-    maybe_rescale(mt_next);
-    uint32_t pf[2][2][4];
-    l_run += softmax_p(s_next, pf, k_len - (nkt - 1) * BN);
+  };
+  // last tile: keys past the segment end are masked out of the row sum
+  auto last = [&](const f32x16_t (&s)[QB][2]) {
+    const int valid = k_len - (nkt - 1) * BN;
+    uint32_t pf[QB][2][2][4];
+    float rs[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s[qb], pf[qb], m_run[qb], valid);
+    if (needs_rescale(rs)) rescale_tile((nkt - 1) % 3, pf, rs, valid);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
     pv((nkt - 1) & 1, pf);
+  };
+#if ATTN_SCHED
+  // The two score register sets swap roles every tile, so each trip of the
+  // loop runs two tiles and no scores are copied between iterations.
+  f32x16_t s_alt[QB][2];
+  int kt = 0;
+  for (; kt + 2 < nkt; kt += 2) {
+    steady(kt, s_next, s_alt);
+    steady(kt + 1, s_alt, s_next);
   }
+  if (nkt > 0) {
+    if (kt + 1 < nkt) {
+      steady(kt, s_next, s_alt);
+      last(s_alt);
+    } else {
+      last(s_next);
+    }
+  }
+#else
+  // P(kt) is complete before S(kt+1) is computed: one score register set
+  for (int kt = 0; kt + 1 < nkt; ++kt) steady(kt, s_next, s_next);
+  if (nkt > 0) last(s_next);
+#endif
 
   // ---- normalise and store
-  const float l = l_run + __shfl_xor(l_run, 32, 64);
-  if (qrow < q_end) {
-    const float inv = (l > 0.f) ? 1.f / l : 0.f;
-    bf16_t* orow = O + (int64_t)qrow * ldo + (int64_t)head * HD;
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    const int qrow = qrow0 + 32 * qb;
+    if (qrow < q_end) {
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      bf16_t* orow = O + (int64_t)qrow * ldo + (int64_t)head * HD;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dd = d * 32 + g * 8 + hh * 4;
-        u32x2_t w = u32x2_t{pack_bf2(o[d][g * 4 + 0] * inv, o[d][g * 4 + 1] * inv),
-                            pack_bf2(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2_t*>(orow + dd) = w;
-      }
-    if (lse != nullptr && hh == 0)
-      lse[(int64_t)head * lse_ld + qrow] = (l > 0.f) ? (m_run + log2f(l)) * 0.6931471805599453f : -INFINITY;
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = d * 32 + g * 8 + hh * 4;
+          u32x2_t w = u32x2_t{pack_bf2(o[qb][d][g * 4 + 0] * inv, o[qb][d][g * 4 + 1] * inv),
+                              pack_bf2(o[qb][d][g * 4 + 2] * inv, o[qb][d][g * 4 + 3] * inv)};
+          *reinterpret_cast<u32x2_t*>(orow + dd) = w;
+        }
+      if (lse != nullptr && hh == 0)
+        lse[(int64_t)head * lse_ld + qrow] = (l > 0.f) ? (m_run[qb] + log2f(l)) * 0.6931471805599453f : -INFINITY;
+    }
   }
 }
 
@@ -461,6 +572,8 @@ DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k
   DITK_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)vt % 16) == 0 &&
                ((uintptr_t)o % 8) == 0, "ditk_flash_attn_varlen: misaligned tensor");
   DITK_REQUIRE(softmax_scale > 0.f, "ditk_flash_attn_varlen: softmax_scale must be > 0");
+  // the kernel addresses a 64-row K tile and an HD-row Vt tile with 32-bit element offsets
+  DITK_REQUIRE(ldk < (1ll << 24) && vt_ld < (1ll << 24), "ditk_flash_attn_varlen: ldk / vt_ld too large");
   if (Tq == 0) return 0;
   const float sl2 = softmax_scale * 1.4426950408889634f;
   const int64_t hs = (int64_t)head_dim * vt_ld;
@@ -476,9 +589,9 @@ DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k
   };
   int rc;
   if (head_dim == 128)
-    rc = run(flash_fwd_kernel<128, ATTN_NW>, ATTN_NW * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   else
-    rc = run(flash_fwd_kernel<64, ATTN_NW>, ATTN_NW * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
 }

@@ -39,9 +39,6 @@ constexpr int BN = 64;   // keys per iteration
 #ifndef ATTN_QB
 #define ATTN_QB 1        // 32-query blocks per wave
 #endif
-#ifndef ATTN_SCHED
-#define ATTN_SCHED 0     // steady loop: 1 = fenced MFMA/VALU interleave, 0 = compiler order
-#endif
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 constexpr float kRescaleSum = 256.0f;  // 2^kLazy: a lane's row sum above it triggers a rescale
 
@@ -97,8 +94,8 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 //   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) = exp2(S(kt) c - m) on VALU
 //   B: O += Vt(kt) P(kt) on MFMA
 // Each K / Vt fragment read from LDS feeds QB MFMAs (one per 32-query block).
-// K(kt) sits in LDS stage kt % 3 (kept resident for the rescale path while
-// K(kt+2) streams in), Vt(kt) in stage kt % 2.
+// K(kt) sits in LDS stage kt % KST (kept resident for the rescale path while
+// later tiles stream in), Vt(kt) in stage kt % 2.
 template <int HD, int NW, int QB>
 __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
@@ -112,7 +109,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   constexpr int K_LOADS = BN * KCH / 64 / NW;   // 64-slot DMA groups per wave
   constexpr int V_LOADS = HD * 8 / 64 / NW;
   static_assert(K_LOADS >= 1 && V_LOADS >= 1 && (BN * KCH / 64) % NW == 0, "tile too small for the workgroup");
-  __shared__ u32x4_t Ks[3][BN * KCH];
+  constexpr int KST = 3;  // K stages in LDS
+  __shared__ u32x4_t Ks[KST][BN * KCH];
   __shared__ u32x4_t Vs[2][HD * 8];
 
   // XCD-aware order: hardware deals workgroup ids round-robin over 8 XCDs, so
@@ -335,6 +333,22 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   // tile's row sum has to skip them.
   const int nkt = (k_len + BN - 1) / BN;
   f32x16_t s_next[QB][2];
+  // last tile: keys past the segment end are masked out of the row sum
+  auto last = [&](const f32x16_t (&s)[QB][2]) {
+    const int valid = k_len - (nkt - 1) * BN;
+    uint32_t pf[QB][2][2][4];
+    float rs[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s[qb], pf[qb], m_run[qb], valid);
+    if (needs_rescale(rs)) rescale_tile((nkt - 1) % KST, pf, rs, valid);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
+    pv((nkt - 1) & 1, pf);
+  };
+  // Per tile: P(kt) on VALU, the (rare) rescale, S(kt+1) and PV(kt) on MFMA, in
+  // compiler order with one score register set; with two waves per SIMD one
+  // wave's MFMAs overlap the other's exp2.  K DMA runs two tiles ahead through
+  // three stages, Vt one tile ahead through two.
   if (nkt > 0) {
     issue_k(0, 0);
     dma_wait();
@@ -347,127 +361,24 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     dma_wait();
     __syncthreads();
   }
-
-  // Steady-state iteration for tile kt (never the last tile, so all 64 keys are
-  // valid).  ATTN_SCHED 1: scheduling-fenced groups, K(kt+1) chunks read four
-  // ahead, each group = the MFMAs of one K chunk for all query blocks and
-  // 16*QB/NC score pairs of P(kt); Vt(kt) reads two groups ahead of the PV MFMAs.
-  // ATTN_SCHED 0: P(kt), then S(kt+1), then PV, scheduled by the compiler.
-  auto steady = [&](int kt, const f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2]) {
-    const int kcur = kt % 3, knxt = (kt + 1) % 3, vcur = kt & 1;
-    if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % 3);
+  for (int kt = 0; kt + 1 < nkt; ++kt) {  // every tile but the last: all 64 keys valid
+    const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
+    if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);
     issue_v(kt + 1, vcur ^ 1);
     uint32_t pf[QB][2][2][4];
     float rs[QB];
-#if ATTN_SCHED
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      rs[qb] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s_nxt[qb][kk][v] = 0.f;
-    }
-    bf16x8_t kf[NC][2];
-    auto read_k = [&](int c) {
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) kf[c][kk] = k_frag(knxt, c, kk);
-    };
-    constexpr int KAHEAD = NC < 4 ? NC : 4;
-#pragma unroll
-    for (int c = 0; c < KAHEAD; ++c) read_k(c);
-    __builtin_amdgcn_sched_barrier(0);
-    constexpr int PAIRS = 16 * QB / NC;  // score pairs of P(kt) per group
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (c + KAHEAD < NC) read_k(c + KAHEAD);
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c][kk], qf[qb][c], s_nxt[qb][kk], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < PAIRS; ++i) {
-        const int pi = c * PAIRS + i, qb = pi >> 4, kk = (pi >> 3) & 1, j = (pi >> 2) & 1, e = pi & 3;
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
-        pf[qb][kk][j][e] = pack_bf2(p0, p1);
-        rs[qb] += p0 + p1;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s_next[qb], pf[qb], m_run[qb], BN);
     pin(pf);
     if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
-    bf16x8_t vf[4][DT];
-    auto read_v = [&](int g) {
-#pragma unroll
-      for (int d = 0; d < DT; ++d) vf[g][d] = v_frag(vcur, g, d);
-    };
-    read_v(0);
-    read_v(1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      if (g + 2 < 4) read_v(g + 2);
-#pragma unroll
-      for (int d = 0; d < DT; ++d)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const uint32_t* p = pf[qb][g >> 1][g & 1];
-          const u32x4_t p4 = u32x4_t{p[0], p[1], p[2], p[3]};
-          o[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[g][d], __builtin_bit_cast(bf16x8_t, p4), o[qb][d], 0, 0, 0);
-        }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#else
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s_cur[qb], pf[qb], m_run[qb], BN);
-    pin(pf);
-    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
-    compute_s(knxt, s_nxt);
+    compute_s(knxt, s_next);
     pv(vcur, pf);
-#endif
     dma_wait();
     __syncthreads();
-  };
-  // last tile: keys past the segment end are masked out of the row sum
-  auto last = [&](const f32x16_t (&s)[QB][2]) {
-    const int valid = k_len - (nkt - 1) * BN;
-    uint32_t pf[QB][2][2][4];
-    float rs[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s[qb], pf[qb], m_run[qb], valid);
-    if (needs_rescale(rs)) rescale_tile((nkt - 1) % 3, pf, rs, valid);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
-    pv((nkt - 1) & 1, pf);
-  };
-#if ATTN_SCHED
-  // The two score register sets swap roles every tile, so each trip of the
-  // loop runs two tiles and no scores are copied between iterations.
-  f32x16_t s_alt[QB][2];
-  int kt = 0;
-  for (; kt + 2 < nkt; kt += 2) {
-    steady(kt, s_next, s_alt);
-    steady(kt + 1, s_alt, s_next);
   }
-  if (nkt > 0) {
-    if (kt + 1 < nkt) {
-      steady(kt, s_next, s_alt);
-      last(s_alt);
-    } else {
-      last(s_next);
-    }
-  }
-#else
-  // P(kt) is complete before S(kt+1) is computed: one score register set
-  for (int kt = 0; kt + 1 < nkt; ++kt) steady(kt, s_next, s_next);
   if (nkt > 0) last(s_next);
-#endif
 
   // ---- normalise and store
 #pragma unroll

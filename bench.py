@@ -3,10 +3,12 @@
 (2 x 32760 tokens), bf16, on one MI355X.
 
 A step = packed prelude for the (cond, uncond) pair + 30 DiT blocks + prediction
-+ CFG combine + a flow-matching Euler update, all on the ditk HIP kernels.
++ the fused CFG combine and UniPC update (Wan's scheduler recipe: flow sigmas,
+shift 3.0, 50-step schedule, order 2 with corrector), all on the ditk HIP kernels.
+The model timestep of each step is the schedule's (999, 997, ...).
 Synthetic data: random-init weights N(0, 0.02^2) (norm weights N(1, 0.02^2)),
 latent 16x21x60x104 N(0,1), text contexts 512x4096 N(0,1) with 120 (cond) and 0
-(uncond) valid rows, timestep 999.
+(uncond) valid rows.
 
 Prints one JSON line (rank 0).  `roofline` is for the dominant kernel, the
 self-attention flash kernel, from HIP events recorded on its launch stream over
@@ -23,9 +25,9 @@ METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFM
 PEAK_BF16_TFLOPS = 2500.0
 LATENT = (16, 21, 60, 104)
 TEXT_VALID = (120, 0)
-TIMESTEP = 999.0
 GUIDANCE = 5.0
-EULER_DT = -1.0 / 50.0
+FLOW_SHIFT = 3.0
+SCHEDULE_STEPS = 50
 CALIB_BYTES = 256 << 20
 # A100-PCIe-40GB, fp16, same workload: 3964.62 ms per step (the reference's published figure)
 REFERENCE_STEPS_PER_S = 1000.0 / 3964.62
@@ -91,8 +93,8 @@ def main():
 
     import torch
 
-    from ditserve_amd import ops
     from ditserve_amd.profiling import EventProfiler
+    from ditserve_amd.solver import UniPCFlowScheduler
     from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer, step_flops
 
     cfg = WAN21_T2V_1_3B
@@ -111,10 +113,13 @@ def main():
     calib_src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     calib_dst = torch.empty_like(calib_src)
 
+    sched = UniPCFlowScheduler(flow_shift=FLOW_SHIFT)
+    sched.set_timesteps(max(SCHEDULE_STEPS, args.warmup + args.steps))
+
     def step(lat):
-        cond, uncond = model.forward_packed([lat, lat], [TIMESTEP, TIMESTEP], texts)
-        v = ops.cfg_combine(cond, uncond, GUIDANCE)
-        return lat + EULER_DT * v
+        t = float(sched.timesteps[sched.step_index])
+        cond, uncond = model.forward_packed([lat, lat], [t, t], texts)
+        return sched.step(cond, t, lat, uncond=uncond, guidance=GUIDANCE)[0]
 
     for _ in range(args.warmup):
         latent = step(latent)
@@ -156,7 +161,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: random-init weights N(0,0.02^2), latent/text N(0,1)",
         "config": {"workload": "Wan2.1-T2V-1.3B-architecture denoise step, latent 16x21x60x104 (480x832x81f), "
-                               "CFG pair packed as 2 x 32760 tokens, 30 blocks, text 512 (valid 120/0), t=999",
+                               "CFG pair packed as 2 x 32760 tokens, 30 blocks, text 512 (valid 120/0), UniPC flow-shift-3 "
+                               "50-step schedule (t = 999, 997, ...)",
                    "tokens_per_step": 2 * seq, "blocks": cfg.layers},
         "tokens_per_s": 2 * seq * 1000.0 / ms,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,

@@ -63,6 +63,40 @@ __global__ void cfg_combine_kernel(const float* __restrict__ cond, const float* 
     out[i] = uncond[i] + g * (cond[i] - uncond[i]);
 }
 
+// Fused CFG combine + solver step over one request's latent (fp32), with the
+// step's scalar coefficients computed on the host:
+//   v  = uncond ? u + g (c - u) : c          CFG combine
+//   m  = x - sigma v                          data (x0) prediction of a flow model
+//   xc = ax x + a0 xl + a1 mp + a2 mp2 + a3 m corrected sample at sigma
+//   xn = b0 xc + b1 m + b2 mp + bv v          predicted sample at the next sigma
+// xl / mp / mp2 (last sample, previous two data predictions) are read only when
+// their coefficients are non-zero, so they may be null otherwise.  xn may alias x,
+// xc may alias xl and m may alias mp2: each element is read before it is written.
+struct SolverCoef {
+  float g, sigma, ax, a0, a1, a2, a3, b0, b1, b2, bv;
+  int use_uncond, use_xl, use_mp, use_mp2;
+};
+
+__global__ void solver_step_kernel(const float* x, const float* __restrict__ c,
+                                   const float* __restrict__ u, const float* xl, const float* mp,
+                                   const float* mp2, float* xn, float* xc_out, float* m_out, int64_t n,
+                                   SolverCoef k) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float xi = x[i];
+    const float ci = c[i];
+    const float v = k.use_uncond ? fmaf(k.g, ci - u[i], u[i]) : ci;
+    const float m = fmaf(-k.sigma, v, xi);
+    const float xl_i = k.use_xl ? xl[i] : 0.f;
+    const float mp_i = k.use_mp ? mp[i] : 0.f;
+    const float mp2_i = k.use_mp2 ? mp2[i] : 0.f;
+    const float xc = k.ax * xi + k.a0 * xl_i + k.a1 * mp_i + k.a2 * mp2_i + k.a3 * m;
+    const float xnext = k.b0 * xc + k.b1 * m + k.b2 * mp_i + k.bv * v;
+    if (xc_out) xc_out[i] = xc;
+    if (m_out) m_out[i] = m;
+    xn[i] = xnext;
+  }
+}
+
 // joint[cu_joint[m] + r] = img[cu_img[m] + r] for r < n_img(m), then txt rows.
 // direction 0: gather (img, txt -> joint); 1: scatter (joint -> img, txt).
 __global__ void joint_copy_kernel(bf16_t* __restrict__ img, int64_t ld_img, bf16_t* __restrict__ txt,
@@ -158,4 +192,23 @@ DITK_EXPORT int ditk_silu(const void* x, void* y, int64_t n, hipStream_t stream)
   if (n == 0) return 0;
   silu_kernel<<<grid_for(n), 256, 0, stream>>>((const bf16_t*)x, (bf16_t*)y, n);
   return ditk_check_launch("ditk_silu");
+}
+
+DITK_EXPORT int ditk_solver_step(const float* x, const float* cond, const float* uncond, const float* x_last,
+                                 const float* m_prev, const float* m_prev2, float* x_next, float* x_corr,
+                                 float* m_out, int64_t n, const float* coef, hipStream_t stream) {
+  DITK_REQUIRE(x && cond && x_next && coef && n >= 0, "ditk_solver_step: bad arguments");
+  SolverCoef k;
+  k.g = coef[0]; k.sigma = coef[1]; k.ax = coef[2]; k.a0 = coef[3]; k.a1 = coef[4]; k.a2 = coef[5];
+  k.a3 = coef[6]; k.b0 = coef[7]; k.b1 = coef[8]; k.b2 = coef[9]; k.bv = coef[10];
+  k.use_uncond = uncond != nullptr;
+  k.use_xl = k.a0 != 0.f;
+  k.use_mp = k.a1 != 0.f || k.b2 != 0.f;
+  k.use_mp2 = k.a2 != 0.f;
+  DITK_REQUIRE((!k.use_xl || x_last) && (!k.use_mp || m_prev) && (!k.use_mp2 || m_prev2),
+               "ditk_solver_step: a history buffer with a non-zero coefficient is null");
+  if (n == 0) return 0;
+  solver_step_kernel<<<grid_for(n), 256, 0, stream>>>(x, cond, uncond, x_last, m_prev, m_prev2, x_next, x_corr,
+                                                      m_out, n, k);
+  return ditk_check_launch("ditk_solver_step");
 }

@@ -6,6 +6,7 @@ workers/xfuser/core/attention/spec.py:244-246), allocates outputs with
 ``torch.empty`` when none is given, and launches on the caller's current
 stream without synchronising.  There is no CPU or PyTorch fallback.
 """
+import ctypes
 import math
 
 import torch
@@ -340,6 +341,34 @@ def cfg_combine(cond, uncond, guidance):
     _lib.call("ditk_cfg_combine", _ptr(cond.contiguous()), _ptr(uncond.contiguous()), _ptr(out), cond.numel(),
               float(guidance), _stream())
     return out
+
+
+def solver_step(x, cond, coef, uncond=None, x_last=None, m_prev=None, m_prev2=None, x_next=None, x_corr=None,
+                m_out=None):
+    """Fused CFG combine + solver update (ditk_solver_step) on fp32 latents.
+
+    coef: 11 floats {g, sigma, ax, a0, a1, a2, a3, b0, b1, b2, bv}.  Returns x_next
+    (new tensor unless given; may be x itself)."""
+    if len(coef) != 11:
+        raise ValueError("solver_step: coef needs 11 values")
+    _check(x, "x", torch.float32)
+    _check(cond, "cond", torch.float32)
+    n = x.numel()
+    for name, t in (("cond", cond), ("uncond", uncond), ("x_last", x_last), ("m_prev", m_prev),
+                    ("m_prev2", m_prev2), ("x_next", x_next), ("x_corr", x_corr), ("m_out", m_out)):
+        if t is not None:
+            _check(t, name, torch.float32)
+            if t.numel() != n or not t.is_contiguous():
+                raise ValueError(f"solver_step: {name} must be contiguous with {n} elements")
+    if not x.is_contiguous():
+        raise ValueError("solver_step: x must be contiguous")
+    if x_next is None:
+        x_next = torch.empty_like(x)
+    arr = (ctypes.c_float * 11)(*[float(c) for c in coef])
+    opt = lambda t: _ptr(t) if t is not None else None  # noqa: E731
+    _lib.call("ditk_solver_step", _ptr(x), _ptr(cond), opt(uncond), opt(x_last), opt(m_prev), opt(m_prev2),
+              _ptr(x_next), opt(x_corr), opt(m_out), n, ctypes.addressof(arr), _stream())
+    return x_next
 
 
 def joint_gather(img, txt, seg_img, seg_txt, out=None):

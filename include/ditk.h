@@ -142,6 +142,24 @@ int ditk_joint_copy(void* img, int64_t ld_img, void* txt, int64_t ld_txt, void* 
 /* y = silu(x), bf16.  Replaces: the SiLU before time_proj / AdaLN linears. */
 int ditk_silu(const void* x, void* y, int64_t n, ditk_stream_t stream);
 
+/*
+ * Fused CFG combine + solver step for one request's fp32 latent of n elements,
+ * with the step's scalar coefficients coef[11] = {g, sigma, ax, a0, a1, a2, a3,
+ * b0, b1, b2, bv} computed on the host:
+ *   v  = uncond ? u + g (c - u) : c;   m = x - sigma v
+ *   x_corr = ax x + a0 x_last + a1 m_prev + a2 m_prev2 + a3 m
+ *   x_next = b0 x_corr + b1 m + b2 m_prev + bv v
+ * (UniPC predictor/corrector on flow sigmas, or FlowMatch-Euler with ax = b0 = 1,
+ * bv = sigma_next - sigma.)  History pointers may be null where their
+ * coefficients are zero; x_corr / m_out may be null (not written).  x_next may
+ * alias x, x_corr may alias x_last, m_out may alias m_prev2.
+ * Replaces: CFG combine + scheduler.step — workers/ditserve/models/wan/block.py:465-483,
+ *   workers/ditserve/models/wan/runtime.py:686-701, workers/ditserve/models/sd35.py:942-953.
+ */
+int ditk_solver_step(const float* x, const float* cond, const float* uncond, const float* x_last,
+                     const float* m_prev, const float* m_prev2, float* x_next, float* x_corr, float* m_out,
+                     int64_t n, const float* coef, ditk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

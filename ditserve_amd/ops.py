@@ -164,6 +164,15 @@ class Rope:
             if g[0] * g[1] * g[2] != n:
                 raise ValueError(f"grid {g} does not cover segment of {n} tokens")
 
+    def __iter__(self):
+        """The tensors a packet codec carries for the rotation: the two angle
+        tables.  The per-token rotation is rebuilt from them and the packet's
+        per-request grids."""
+        return iter((self.cos, self.sin))
+
+    def __len__(self):
+        return 2
+
 
 def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None):
     """In place: RMSNorm(q), RMSNorm(k) (across all heads, or per head) then 3D RoPE.

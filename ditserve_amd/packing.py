@@ -26,13 +26,21 @@ def packing_stats(heights, widths, *, vae_scale_factor=8, patch_size=2):
         if h <= 0 or w <= 0 or h % stride or w % stride:
             raise ValueError(f"resolution ({h}, {w}) must be positive and divisible by {stride}")
     counts = [(h // stride) * (w // stride) for h, w in res]
-    cu = build_cu_seqlens(counts)
-    padded = len(counts) * max(counts)
-    saved = padded - cu[-1]
     return {
         "batch_size": len(counts),
         "heterogeneous_resolutions": len(set(res)) > 1,
         "resolutions": [list(r) for r in res],
+        **token_packing_stats(counts),
+    }
+
+
+def token_packing_stats(counts):
+    """cu_seqlens and padding savings of a packed batch of token counts."""
+    counts = [int(n) for n in counts]
+    cu = build_cu_seqlens(counts)
+    padded = len(counts) * max(counts)
+    saved = padded - cu[-1]
+    return {
         "image_token_counts": counts,
         "cu_seqlens": cu,
         "max_seqlen": max(counts),

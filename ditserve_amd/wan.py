@@ -260,9 +260,39 @@ class WanTransformer:
         t = torch.tensor([float(x) for x in timesteps], dtype=torch.float32, device=dev)
         temb, projected, enc = self.condition(t, text)
         rope = ops.Rope(self.rope_cos, self.rope_sin, grids, seg, self.rope_pairs[0], self.rope_pairs[1])
-        return dict(hidden=hidden, encoder=enc, temb=temb, projected=projected, rotary=rope,
-                    shape=[(1, *g, *cfg.patch) for g in grids], pad_amount=0, local_rows=0, valid_kv_len=None,
-                    thw=grids, cu_seqlens_q=seg, cu_seqlens_kv_text=seg_txt, grids=grids)
+        packet = dict(hidden=hidden, encoder=enc, temb=temb, projected=projected, rotary=rope,
+                      shape=[(1, *g, *cfg.patch) for g in grids], pad_amount=0, local_rows=0, valid_kv_len=None,
+                      thw=[list(g) for g in grids], cu_seqlens_q=seg, cu_seqlens_kv_text=seg_txt, grids=grids)
+        if len(set(text_lens)) > 1:
+            packet["text_lens"] = text_lens
+        return packet
+
+    def resolve_packet(self, packet):
+        """Rebuild the derived entries of a packet that was carried by a codec
+        (workers/ditserve/models/wan/block.py:885-1007): only hidden, encoder, temb,
+        projected, rotary (tensors), shape and thw (lists) travel; the segment
+        tables, grids and RoPE object follow from them.  Idempotent."""
+        if isinstance(packet.get("rotary"), ops.Rope) and "cu_seqlens_q" in packet:
+            return packet
+        grids = [tuple(int(v) for v in g) for g in packet["thw"]]
+        counts = [g[0] * g[1] * g[2] for g in grids]
+        seg = Segments([0] + [sum(counts[: i + 1]) for i in range(len(counts))], self.device)
+        if seg.total != packet["hidden"].shape[0]:
+            raise ValueError("packet grids do not match its hidden rows")
+        text_lens = packet.get("text_lens")
+        if text_lens is None:
+            rows = packet["encoder"].shape[0]
+            if rows % len(grids):
+                raise ValueError("non-uniform text lengths need the packet's text_lens")
+            text_lens = [rows // len(grids)] * len(grids)
+        seg_txt = Segments([0] + [sum(text_lens[: i + 1]) for i in range(len(text_lens))], self.device)
+        tables = tuple(packet["rotary"])
+        if len(tables) != 2:
+            raise ValueError("packet rotary must carry the two RoPE angle tables")
+        cos, sin = (t.to(device=self.device, dtype=torch.float32).contiguous() for t in tables)
+        packet.update(rotary=ops.Rope(cos, sin, grids, seg, self.rope_pairs[0], self.rope_pairs[1]),
+                      cu_seqlens_q=seg, cu_seqlens_kv_text=seg_txt, grids=grids)
+        return packet
 
     def begin_packet(self, hidden_states, timestep, encoder_hidden_states):
         """Reference-shaped prelude (transformer_wan.py:307-366) for B requests
@@ -282,6 +312,7 @@ class WanTransformer:
         """One block over the packed batch; returns and stores the new hidden."""
         cfg, blk, prof = self.cfg, self.blocks[index], self.profiler
         D, H, Dh = cfg.dim, cfg.heads, cfg.head_dim
+        self.resolve_packet(packet)
         seg, seg_txt = packet["cu_seqlens_q"], packet["cu_seqlens_kv_text"]
         h = packet["hidden"]
         with prof.region("modulation+adaln"):
@@ -326,6 +357,7 @@ class WanTransformer:
     def prediction_packed(self, packet):
         """norm_out AdaLN + proj_out + unpatchify per request -> list of fp32 [C, F, H, W]."""
         cfg = self.cfg
+        self.resolve_packet(packet)
         seg = packet["cu_seqlens_q"]
         # (scale_shift_table [2, D] + temb[:, None]) -> shift, scale   (block.py:441-445)
         temb = packet["temb"].float().reshape(-1, 1, cfg.dim).expand(-1, 2, -1)

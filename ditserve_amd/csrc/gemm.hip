@@ -21,6 +21,10 @@
 // per-request projections agree bitwise.
 #include "ditk_common.h"
 
+#ifndef GEMM_WAVES
+#define GEMM_WAVES 8  // waves per workgroup (4: one per SIMD, 8: two per SIMD)
+#endif
+
 namespace {
 
 enum Epilogue : int {
@@ -36,6 +40,11 @@ constexpr int GBM = 256;    // tokens per workgroup tile
 constexpr int GBN = 256;    // features per workgroup tile
 constexpr int GBK = 32;     // k per LDS stage (4 x 16-byte chunks per row)
 constexpr int NSTAGE = 4;   // LDS stages: 3 k-steps of DMA in flight
+constexpr int GW = GEMM_WAVES;               // waves per workgroup: 2 x (GW/2) wave tiles
+constexpr int WTM = GBM / 2;                 // tokens per wave tile
+constexpr int WTN = GBN / (GW / 2);          // features per wave tile
+constexpr int NI = WTN / 32, NJ = WTM / 32;  // 32x32 MFMA tiles per wave tile
+constexpr int DPW = 16 / GW;                 // DMA instructions per operand, wave and stage
 
 constexpr int GROUP_M = 8;  // m-tiles per tile-order group (L2 reuse of W)
 
@@ -45,10 +54,11 @@ __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
                                    (__attribute__((address_space(3))) void*)lds_slot0, 16, 0, 0);
 }
-// wait until at most n (0, 8 or 16) of this wave's DMA instructions are in flight
-__device__ __forceinline__ void dma_wait_le(int n) {
-  if (n >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+// wait until at most `stages` DMA stages (2*DPW instructions each) of this wave are in flight
+__device__ __forceinline__ void dma_wait_stages(int stages) {
+  constexpr int P = 2 * (16 / GEMM_WAVES);
+  if (stages >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * P) : "memory");
+  else if (stages == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(P) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
@@ -57,13 +67,13 @@ __device__ __forceinline__ void dma_wait_le(int n) {
 // 16 rows x 64 contiguous bytes; 16 consecutive lanes reading chunk u of 16
 // consecutive rows hit 16 distinct bank groups.
 template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(
+__global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n) {
   // 128 KiB of LDS: NSTAGE stages of A and W tiles; reused by the epilogue as
-  // one 128x128 bf16 staging tile per wave.
+  // one [WTM tokens][WTN features] bf16 staging tile per wave.
   __shared__ u32x4_t lds[NSTAGE * (GBM + GBN) * 4];
   auto As = [&](int s) { return lds + s * (GBM * 4); };
   auto Ws = [&](int s) { return lds + NSTAGE * GBM * 4 + s * (GBN * 4); };
@@ -84,7 +94,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const int wm = wave_u & 1, wn = wave_u >> 1;
+  const int wm = wave_u & 1, wn = wave_u >> 1;  // wave tile: tokens wm*WTM.., features wn*WTN..
 
   // ---- DMA source offsets (elements, per lane, loop invariant).  Group g of
   // 64 slots covers rows 16g..16g+15; lane l -> row 16g + l/4, stored chunk
@@ -92,10 +102,10 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   const bf16_t* Ablk = A + (int64_t)m0 * lda;
   const bf16_t* Wblk = W + (int64_t)n0 * ldw;
   const int lsw = ((lane & 3) ^ ((lane >> 4) & 3)) * 8;
-  uint32_t a_off[4], w_off[4];  // element offsets within the workgroup's row block
+  uint32_t a_off[DPW], w_off[DPW];  // element offsets within the workgroup's row block
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = i * 4 + wave_u;
+  for (int i = 0; i < DPW; ++i) {
+    const int g = i * GW + wave_u;
     const int row = g * 16 + (lane >> 2);
     a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + lsw);
     w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + lsw);
@@ -105,8 +115,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
     const bf16_t* a = Ablk + kt * GBK;
     const bf16_t* w = Wblk + kt * GBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int g = i * 4 + wave_u;
+    for (int i = 0; i < DPW; ++i) {
+      const int g = i * GW + wave_u;
       lds_dma16(a + a_off[i], &As(s)[g * 64]);
       lds_dma16(w + w_off[i], &Ws(s)[g * 64]);
     }
@@ -119,43 +129,47 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
 #pragma unroll
     for (int c = 0; c < 2; ++c) rbase[c] = l32 * 4 + ((c * 2 + hh) ^ sg);
   }
-  const int a_row0 = wm * 128, w_row0 = wn * 128;
+  const int a_row0 = wm * WTM, w_row0 = wn * WTN;
 
-  f32x16_t acc[4][4];  // [feature tile i][token tile j]
+  f32x16_t acc[NI][NJ];  // [feature tile i][token tile j]
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int nk = K / GBK;
-  auto read_chunk = [&](int s, int c, bf16x8_t (&af)[4], bf16x8_t (&bf)[4]) {
+  auto read_chunk = [&](int s, int c, bf16x8_t (&af)[NI], bf16x8_t (&bf)[NJ]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      af[i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + i * 32) * 4]);
-      bf[i] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + i * 32) * 4]);
-    }
+    for (int i = 0; i < NI; ++i) af[i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + i * 32) * 4]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) bf[j] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + j * 32) * 4]);
   };
-  auto mfma_chunk = [&](const bf16x8_t (&af)[4], const bf16x8_t (&bf)[4]) {
+  auto mfma_chunk = [&](const bf16x8_t (&af)[NI], const bf16x8_t (&bf)[NJ]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  };
+  // operand read r (0 .. NI+NJ-1) of chunk c from stage s into (af, bf)
+  auto read_one = [&](int s, int c, int r, bf16x8_t (&af)[NI], bf16x8_t (&bf)[NJ]) {
+    if (r < NI) af[r] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + r * 32) * 4]);
+    else bf[r - NI] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + (r - NI) * 32) * 4]);
   };
 
   // Pipeline: stages kt+1..kt+3 of DMA in flight; the barrier that publishes
   // stage kt+1 and the first operand reads from it sit between the two MFMA
-  // batches of stage kt, so the MFMA pipe keeps draining through them.  Every
-  // wave waits for its own DMA with vmcnt before the barrier, so a plain
-  // s_barrier (no release fence, which would drain all stages in flight)
-  // publishes the stage.
+  // halves of stage kt.  Every wave waits for its own DMA with vmcnt before
+  // the barrier, so a plain s_barrier (no release fence, which would drain all
+  // stages in flight) publishes the stage.  Two waves per SIMD: while one waits
+  // to issue its DMA into the memory pipeline, the other one's MFMAs issue.
 #pragma unroll
   for (int kt = 0; kt < NSTAGE - 1; ++kt)
     if (kt < nk) issue(kt);
-  bf16x8_t fa0[4], fb0[4], fa1[4], fb1[4];
-  dma_wait_le(8 * min(NSTAGE - 2, nk - 1));
+  bf16x8_t fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
+  dma_wait_stages(min(NSTAGE - 2, nk - 1));
   __syncthreads();
   read_chunk(0, 0, fa0, fb0);
 
@@ -163,38 +177,44 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
   };
+  constexpr int NM = NI * NJ;         // MFMAs per chunk
+  constexpr int NR = NI + NJ;         // operand reads per chunk
+  constexpr int NQ = NM / 2;          // groups of 2 MFMAs per chunk
+  static_assert(NR <= 2 * NQ && 2 * DPW <= NQ * 2, "interleave pattern");
   int kt = 0;
-  // steady state: a DMA stage to issue every iteration.  The MFMAs, the next
-  // operand reads and the DMA issues are interleaved in fixed groups (2 MFMA,
-  // 1 ds_read, 1 DMA) fenced by sched_barrier, so DMA issue never stalls a
-  // long run of MFMAs.
+  // steady state: a DMA stage to issue every iteration.  MFMAs, the next
+  // chunk's operand reads and the DMA issues are interleaved in fixed groups
+  // fenced by sched_barrier, so DMA issue never stalls a long run of MFMAs.
   for (; kt + NSTAGE - 1 < nk; ++kt) {
     const int s = kt % NSTAGE;
     const int sn = (kt + NSTAGE - 1) % NSTAGE;
     const bf16_t* an = Ablk + (kt + NSTAGE - 1) * GBK;
     const bf16_t* wn_ = Wblk + (kt + NSTAGE - 1) * GBK;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      // 2 MFMAs of chunk 0, one operand read of chunk 1, one DMA of stage kt+3
-      const int i0 = (2 * q) / 4, j0 = (2 * q) % 4;
+    for (int q = 0; q < NQ; ++q) {
+      const int x0 = 2 * q, i0 = x0 / NJ, j0 = x0 % NJ;
       acc[i0][j0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[i0], fb0[j0], acc[i0][j0], 0, 0, 0);
       acc[i0][j0 + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[i0], fb0[j0 + 1], acc[i0][j0 + 1], 0, 0, 0);
-      if (q < 4) fa1[q] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[1] + (w_row0 + q * 32) * 4]);
-      else fb1[q - 4] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[1] + (a_row0 + (q - 4) * 32) * 4]);
-      const int g = (q >> 1) * 4 + wave_u;
-      if ((q & 1) == 0) lds_dma16(an + a_off[q >> 1], &As(sn)[g * 64]);
-      else lds_dma16(wn_ + w_off[q >> 1], &Ws(sn)[g * 64]);
+#pragma unroll
+      for (int r = 2 * q; r < 2 * q + 2; ++r)
+        if (r < NR) read_one(s, 1, r, fa1, fb1);
+      if (q < 2 * DPW) {
+        const int d = q >> 1, g = d * GW + wave_u;
+        if ((q & 1) == 0) lds_dma16(an + a_off[d], &As(sn)[g * 64]);
+        else lds_dma16(wn_ + w_off[d], &Ws(sn)[g * 64]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // stage kt+1 landed (this wave)
+    dma_wait_stages(NSTAGE - 2);  // stage kt+1 landed (this wave)
     publish();
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int i0 = (2 * q) / 4, j0 = (2 * q) % 4;
+    for (int q = 0; q < NQ; ++q) {
+      const int x0 = 2 * q, i0 = x0 / NJ, j0 = x0 % NJ;
       acc[i0][j0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[i0], fb1[j0], acc[i0][j0], 0, 0, 0);
       acc[i0][j0 + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[i0], fb1[j0 + 1], acc[i0][j0 + 1], 0, 0, 0);
-      if (q < 4) fa0[q] = __builtin_bit_cast(bf16x8_t, Ws((kt + 1) % NSTAGE)[rbase[0] + (w_row0 + q * 32) * 4]);
-      else fb0[q - 4] = __builtin_bit_cast(bf16x8_t, As((kt + 1) % NSTAGE)[rbase[0] + (a_row0 + (q - 4) * 32) * 4]);
+#pragma unroll
+      for (int r = 2 * q; r < 2 * q + 2; ++r)
+        if (r < NR) read_one((kt + 1) % NSTAGE, 0, r, fa0, fb0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -204,7 +224,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
     read_chunk(s, 1, fa1, fb1);
     mfma_chunk(fa0, fb0);
     if (kt + 1 < nk) {
-      dma_wait_le(8 * (nk - 2 - kt));
+      dma_wait_stages(nk - 2 - kt);
       publish();
       read_chunk((kt + 1) % NSTAGE, 0, fa0, fb0);
     }
@@ -217,11 +237,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
   // f = i*32 + g*8 + hh*4 + e.
   if (EPI == EPI_F32) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int m = m0 + a_row0 + j * 32 + l32;
       if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const int n = n0 + w_row0 + i * 32 + gq * 8 + hh * 4;
@@ -236,14 +256,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
     return;
   }
   // bf16 epilogues: y = bf16(acc + bias) goes through a per-wave LDS tile
-  // [128 tokens][128 features] (16-byte chunk c of row t stored at c ^ (t&15)),
+  // [WTM tokens][WTN features] (16-byte chunk c of row t stored at c ^ (t % CPR)),
   // then rows are read back so residual / gate loads and output stores are
   // 16-byte coalesced.
-  u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * 2048);
-  const u32x4_t* stage16 = lds + wave_u * 2048;
-  static_assert(NSTAGE * (GBM + GBN) * 4 >= 4 * 2048, "epilogue staging needs 128 KiB");
+  constexpr int CPR = WTN / 8;  // 16-byte chunks per staged row
+  u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * (WTM * CPR));
+  const u32x4_t* stage16 = lds + wave_u * (WTM * CPR);
+  static_assert(NSTAGE * (GBM + GBN) * 4 >= GW * WTM * CPR, "epilogue staging exceeds the LDS stages");
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int f = i * 32 + gq * 8 + hh * 4;
@@ -252,24 +273,25 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) b4[e] = (bias != nullptr) ? bias[n + e] : 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int t = j * 32 + l32;
-        const int chunk = (i * 4 + gq) ^ (t & 15);
-        stage8[(t * 16 + chunk) * 2 + hh] =
+        const int chunk = (i * 4 + gq) ^ (t % CPR);
+        stage8[(t * CPR + chunk) * 2 + hh] =
             u32x2_t{pack_bf2(acc[i][j][gq * 4 + 0] + b4[0], acc[i][j][gq * 4 + 1] + b4[1]),
                     pack_bf2(acc[i][j][gq * 4 + 2] + b4[2], acc[i][j][gq * 4 + 3] + b4[3])};
       }
     }
   __syncthreads();
-  const int c = lane & 15;
+  constexpr int RPP = 64 / CPR;  // rows per pass of the wave
+  const int c = lane % CPR;
   const int n = n0 + w_row0 + c * 8;
   if (n >= N) return;
 #pragma unroll 4
-  for (int r = 0; r < 32; ++r) {
-    const int t = r * 4 + (lane >> 4);
+  for (int r = 0; r < WTM / RPP; ++r) {
+    const int t = r * RPP + lane / CPR;
     const int m = m0 + a_row0 + t;
     if (m >= M) continue;
-    u32x4_t v = stage16[t * 16 + (c ^ (t & 15))];
+    u32x4_t v = stage16[t * CPR + (c ^ (t % CPR))];
     if (EPI != EPI_BIAS) {
       float x[8];
       unpack8(v, x);
@@ -310,7 +332,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   const int64_t nblocks = (tiles + 7) / 8 * 8;
   DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
-  gemm_kernel<EPI><<<(unsigned)nblocks, 256, 0, stream>>>(
+  gemm_kernel<EPI><<<(unsigned)nblocks, GW * 64, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
       gate_stride, cu, nseg, tiles_m, tiles_n);
   return ditk_check_launch("ditk_gemm");

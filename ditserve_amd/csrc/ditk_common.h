@@ -101,11 +101,16 @@ __device__ __forceinline__ int find_segment(const int32_t* __restrict__ cu, int 
 }
 
 __device__ __forceinline__ float gelu_tanh_f(float x) {
-  // 0.5 x (1 + tanh(u)) == x * sigmoid(2u),  u = sqrt(2/pi) (x + 0.044715 x^3)
-  const float k0 = 0.7978845608028654f;
-  const float k1 = 0.044715f;
-  float u = k0 * fmaf(k1 * x, x * x, x);
-  return x / (1.0f + __expf(-2.0f * u));
+  // 0.5 x (1 + tanh(u)) == x / (1 + exp(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3);
+  // exp(-2u) = 2^(x (C0 + C1 x^2)) with C0 = -2 sqrt(2/pi) / ln 2, C1 = 0.044715 C0.
+  // v_exp_f32 and v_rcp_f32 (1 ulp each) are far below the bf16 output rounding;
+  // for x -> -inf the power overflows to inf and the result is -0.
+  const float C0 = -2.3022082f, C1 = -0.10294324f;
+  const float e = __builtin_amdgcn_exp2f(x * fmaf(x * x, C1, C0));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) {
+  // x / (1 + e^-x), e^-x = 2^(-x / ln 2)
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950f));
+}

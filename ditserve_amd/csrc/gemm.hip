@@ -258,8 +258,38 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   // bf16 epilogues: y = bf16(acc + bias) goes through a per-wave LDS tile
   // [WTM tokens][WTN features] (16-byte chunk c of row t stored at c ^ (t % CPR)),
   // then rows are read back so residual / gate loads and output stores are
-  // 16-byte coalesced.
-  constexpr int CPR = WTN / 8;  // 16-byte chunks per staged row
+  // 16-byte coalesced.  Lane (c, row group) handles features n..n+7 of rows
+  // t = r*RPP + lane/CPR; its residual rows and gate are loaded before the
+  // staging, so their latency overlaps it instead of stalling each row.
+  constexpr int CPR = WTN / 8;   // 16-byte chunks per staged row
+  constexpr int RPP = 64 / CPR;  // rows per pass of the wave
+  constexpr int NPASS = WTM / RPP;  // passes
+  constexpr bool HAS_RES = EPI == EPI_GATE_RES || EPI == EPI_RES;
+  const int c = lane % CPR;
+  const int n = n0 + w_row0 + c * 8;
+  const int mrow = m0 + a_row0 + lane / CPR;  // row of pass 0; pass r adds r*RPP
+  u32x4_t res[HAS_RES ? NPASS : 1];
+  if (HAS_RES) {
+#pragma unroll
+    for (int r = 0; r < NPASS; ++r) {
+      const int m = mrow + r * RPP;
+      res[r] = (m < M && n < N) ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
+    }
+  }
+  // gate rows: one segment for the whole wave tile (the common case) loads its
+  // gate once; a tile that straddles a segment boundary looks it up per row
+  int seg_lo = 0;
+  bool one_seg = true;
+  f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_GATE_RES) {
+    seg_lo = find_segment(cu, nseg, m0 + a_row0);
+    one_seg = seg_lo == find_segment(cu, nseg, min(m0 + a_row0 + WTM, M) - 1);
+    if (one_seg && n < N) {
+      const float* g = gate + (int64_t)seg_lo * gate_stride + n;
+      g0 = *reinterpret_cast<const f32x4_t*>(g);
+      g1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+    }
+  }
   u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * (WTM * CPR));
   const u32x4_t* stage16 = lds + wave_u * (WTM * CPR);
   static_assert(NSTAGE * (GBM + GBN) * 4 >= GW * WTM * CPR, "epilogue staging exceeds the LDS stages");
@@ -268,10 +298,10 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int f = i * 32 + gq * 8 + hh * 4;
-      const int n = min(n0 + w_row0 + f, N - 4);
+      const int nb = min(n0 + w_row0 + f, N - 4);
       float b4[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b4[e] = (bias != nullptr) ? bias[n + e] : 0.f;
+      for (int e = 0; e < 4; ++e) b4[e] = (bias != nullptr) ? bias[nb + e] : 0.f;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int t = j * 32 + l32;
@@ -282,14 +312,11 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
       }
     }
   __syncthreads();
-  constexpr int RPP = 64 / CPR;  // rows per pass of the wave
-  const int c = lane % CPR;
-  const int n = n0 + w_row0 + c * 8;
   if (n >= N) return;
-#pragma unroll 4
-  for (int r = 0; r < WTM / RPP; ++r) {
+#pragma unroll
+  for (int r = 0; r < NPASS; ++r) {
     const int t = r * RPP + lane / CPR;
-    const int m = m0 + a_row0 + t;
+    const int m = mrow + r * RPP;
     if (m >= M) continue;
     u32x4_t v = stage16[t * CPR + (c ^ (t % CPR))];
     if (EPI != EPI_BIAS) {
@@ -303,15 +330,18 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
         for (int e = 0; e < 8; ++e) x[e] = silu_f(x[e]);
       } else {
         float rv[8];
-        unpack8(*reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n), rv);
+        unpack8(res[HAS_RES ? r : 0], rv);
         if (EPI == EPI_GATE_RES) {
-          const float* g = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
-          const f32x4_t g0 = *reinterpret_cast<const f32x4_t*>(g);
-          const f32x4_t g1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+          f32x4_t h0 = g0, h1 = g1;
+          if (!one_seg) {
+            const float* g = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+            h0 = *reinterpret_cast<const f32x4_t*>(g);
+            h1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            x[e] = fmaf(x[e], g0[e], rv[e]);
-            x[e + 4] = fmaf(x[e + 4], g1[e], rv[e + 4]);
+            x[e] = fmaf(x[e], h0[e], rv[e]);
+            x[e + 4] = fmaf(x[e + 4], h1[e], rv[e + 4]);
           }
         } else {
 #pragma unroll

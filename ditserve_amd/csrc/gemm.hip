@@ -9,12 +9,13 @@
 // activation, so every lane ends up owning one token and 4 consecutive output
 // features per accumulator group -> 8-byte row-major stores.
 //
-// Tiling (gfx950, v_mfma_f32_32x32x16_bf16): a 256-thread workgroup computes a
-// 256 (tokens) x 256 (features) tile as 2x2 waves of 128x128 (16 accumulator
-// tiles per wave, held in AGPRs).  K advances 64 at a time through
-// NSTAGE LDS stages (32 k each) filled by direct global->LDS DMA, with three
-// stages in flight to cover memory latency (no register staging); each
-// stage's operand reads are issued together before its 32 MFMAs.
+// Tiling (gfx950, v_mfma_f32_32x32x16_bf16): a 512-thread workgroup computes a
+// 256 (tokens) x 256 (features) tile as 2 x 4 waves of 128 tokens x 64
+// features (8 accumulator tiles per wave), two waves per SIMD so one wave's
+// MFMAs issue while the other waits to issue its DMA.  K advances 32 at a time
+// through NSTAGE LDS stages filled by direct global->LDS DMA, three stages in
+// flight (no register staging).  The bias is loaded before the k loop, so the
+// epilogue of a bias / GELU / SiLU projection waits on no global load.
 //
 // The k-loop order is fixed and there is no split-K, so every output element is
 // computed the same way whatever M is and wherever its row sits: packed and
@@ -130,6 +131,17 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     for (int c = 0; c < 2; ++c) rbase[c] = l32 * 4 + ((c * 2 + hh) ^ sg);
   }
   const int a_row0 = wm * WTM, w_row0 = wn * WTN;
+
+  // bias of the lane's accumulator features f = i*32 + gq*8 + hh*4 .. +3
+  // (columns past N read the last valid group and are never stored)
+  f32x4_t bvec[NI][4];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+      bvec[i][gq] = bias != nullptr
+                        ? *reinterpret_cast<const f32x4_t*>(bias + min(n0 + w_row0 + i * 32 + gq * 8 + hh * 4, N - 4))
+                        : f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   f32x16_t acc[NI][NJ];  // [feature tile i][token tile j]
 #pragma unroll
@@ -248,7 +260,7 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
           if (n >= N) continue;
           float o[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = acc[i][j][gq * 4 + e] + (bias != nullptr ? bias[n + e] : 0.f);
+          for (int e = 0; e < 4; ++e) o[e] = acc[i][j][gq * 4 + e] + bvec[i][gq][e];
           float* C = reinterpret_cast<float*>(Cv) + (int64_t)m * ldc + n;
           *reinterpret_cast<f32x4_t*>(C) = f32x4_t{o[0], o[1], o[2], o[3]};
         }
@@ -297,11 +309,7 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      const int f = i * 32 + gq * 8 + hh * 4;
-      const int nb = min(n0 + w_row0 + f, N - 4);
-      float b4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) b4[e] = (bias != nullptr) ? bias[nb + e] : 0.f;
+      const f32x4_t b4 = bvec[i][gq];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int t = j * 32 + l32;
@@ -382,8 +390,9 @@ DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw
                "ditk_gemm: lda/ldw must be multiples of 8 and >= K");
   DITK_REQUIRE((int64_t)256 * lda < (1ll << 31) && (int64_t)256 * ldw < (1ll << 31),
                "ditk_gemm: leading dimensions too large");
-  DITK_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)C % 16) == 0,
-               "ditk_gemm: A, W and C must be 16-byte aligned");
+  DITK_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)C % 16) == 0 &&
+                   ((uintptr_t)bias % 16) == 0,
+               "ditk_gemm: A, W, C and bias must be 16-byte aligned");
   DITK_REQUIRE(ldc % 8 == 0 && ldc >= N, "ditk_gemm: ldc must be a multiple of 8 and >= N");
   DITK_REQUIRE(epilogue >= 0 && epilogue <= 5, "ditk_gemm: unknown epilogue %d", epilogue);
   DITK_REQUIRE(!(epilogue == EPI_GATE_RES || epilogue == EPI_RES) ||

@@ -24,7 +24,8 @@ def _seg(cu):
 
 
 # --------------------------------------------------------------------------- GEMM
-GEMM_CASES = [(1000, 1536, 1536), (256, 4608, 1536), (77, 64, 1536), (513, 384, 8960), (33, 1536, 64)]
+GEMM_CASES = [(1000, 1536, 1536), (256, 4608, 1536), (77, 64, 1536), (513, 384, 8960), (33, 1536, 64),
+              (300, 512, 96)]  # K % 64 == 32: the 32-k stage path
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
@@ -72,6 +73,20 @@ def test_gemm_rows_independent_of_packing():
     full = ops.linear(a, w, b)
     part = ops.linear(a[313:777].contiguous(), w, b)
     assert torch.equal(full[313:777], part)
+
+
+def test_gemm_stage_depths_agree():
+    """K % 64 == 0 runs 64-k LDS stages, otherwise 32-k stages; the MFMA k order is
+    the same, so zero-padding K by 32 (forcing the 32-k path) changes no bit."""
+    ops = _ops()
+    M, N, K = 600, 768, 1536
+    a = randn((M, K), 30).to(DEV, torch.bfloat16)
+    w = randn((N, K), 31, 0.02).to(DEV, torch.bfloat16)
+    b = randn((N,), 32).to(DEV)
+    a_pad = torch.cat([a, torch.zeros((M, 32), dtype=a.dtype, device=DEV)], 1).contiguous()
+    w_pad = torch.cat([w, randn((N, 32), 33).to(DEV, torch.bfloat16)], 1).contiguous()
+    assert torch.equal(ops.linear(a, w, b), ops.linear(a_pad, w_pad, b))
+    assert torch.equal(ops.linear(a, w, b, "f32"), ops.linear(a_pad, w_pad, b, "f32"))
 
 
 # --------------------------------------------------------------------------- AdaLN

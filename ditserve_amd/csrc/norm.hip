@@ -17,7 +17,7 @@ constexpr int kMaxChunks = 8;     // 16-byte chunks per lane -> D <= 64*8*8 = 40
 // AdaLN:  y = norm(x) [* w + b] [* (1 + scale[seg]) + shift[seg]]
 //   norm = LayerNorm (kind 0) or RMSNorm (kind 1), eps inside the rsqrt.
 // ---------------------------------------------------------------------------
-template <int KIND>
+template <int KIND, int NC>
 __global__ __launch_bounds__(256) void adaln_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int T, int D,
     const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
@@ -28,42 +28,59 @@ __global__ __launch_bounds__(256) void adaln_kernel(
   if (row >= T) return;
   const int nchunk = D >> 3;
   const bf16_t* xr = x + (int64_t)row * ldx;
-  float v[kMaxChunks][8];
-  float s = 0.f;
+  // Every load of the row is issued before the reductions: the row itself
+  // (NC 16-byte chunks per lane, kept packed), then its segment's scale and
+  // shift (L2-resident), so the latencies overlap.
+  u32x4_t raw[NC];
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = i * 64 + lane;
-    if (c < nchunk) {
-      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(xr + c * 8);
-      unpack8(raw, v[i]);
+  for (int i = 0; i < NC; ++i) {
+    const int c = i * 64 + lane;
+    raw[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(xr + c * 8) : u32x4_t{0, 0, 0, 0};
+  }
+  f32x4_t sc4[NC][2], sh4[NC][2];
+  const bool mod = shift != nullptr;
+  if (mod) {
+    const int seg = find_segment(cu, nseg, row);
+    const float* sh = shift + (int64_t)seg * mod_stride;
+    const float* sc = scale + (int64_t)seg * mod_stride;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += v[i][j];
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(i * 64 + lane, nchunk - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        sc4[i][h] = *reinterpret_cast<const f32x4_t*>(sc + c * 8 + 4 * h);
+        sh4[i][h] = *reinterpret_cast<const f32x4_t*>(sh + c * 8 + 4 * h);
+      }
     }
   }
   float mean = 0.f;
-  if (KIND == 0) mean = wave_sum<64>(s) / (float)D;
+  if (KIND == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      float v[8];
+      unpack8(raw[i], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    mean = wave_sum<64>(s) / (float)D;
+  }
   float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = i * 64 + lane;
-    if (c < nchunk) {
+  for (int i = 0; i < NC; ++i) {
+    if (i * 64 + lane < nchunk) {
+      float v[8];
+      unpack8(raw[i], v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float d = v[i][j] - mean;
+        const float d = v[j] - mean;
         q = fmaf(d, d, q);
       }
     }
   }
   const float rstd = rsqrtf(wave_sum<64>(q) / (float)D + eps);
-  const float* sh = nullptr;
-  const float* sc = nullptr;
-  if (shift != nullptr) {
-    int seg = find_segment(cu, nseg, row);
-    sh = shift + (int64_t)seg * mod_stride;
-    sc = scale + (int64_t)seg * mod_stride;
-  }
   bf16_t* yr = y + (int64_t)row * ldy;
-  // per-column vectors are read as two 16-byte loads per 8-column chunk
+  // affine vectors (not on the modulated path) are read as two 16-byte loads per chunk
   auto load8 = [](const float* p, float* out) {
     const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
     const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + 4);
@@ -74,12 +91,13 @@ __global__ __launch_bounds__(256) void adaln_kernel(
     }
   };
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = i * 64 + lane;
+  for (int i = 0; i < NC; ++i) {
+    const int c = i * 64 + lane;
     if (c < nchunk) {
       float o[8], t[8];
+      unpack8(raw[i], o);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = (v[i][j] - mean) * rstd;
+      for (int j = 0; j < 8; ++j) o[j] = (o[j] - mean) * rstd;
       if (w != nullptr) {
         load8(w + c * 8, t);
 #pragma unroll
@@ -90,12 +108,12 @@ __global__ __launch_bounds__(256) void adaln_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] += t[j];
       }
-      if (sh != nullptr) {
-        float u[8];
-        load8(sc + c * 8, t);
-        load8(sh + c * 8, u);
+      if (mod) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = o[j] * (1.0f + t[j]) + u[j];
+        for (int j = 0; j < 4; ++j) {
+          o[j] = o[j] * (1.0f + sc4[i][0][j]) + sh4[i][0][j];
+          o[j + 4] = o[j + 4] * (1.0f + sc4[i][1][j]) + sh4[i][1][j];
+        }
       }
       *reinterpret_cast<u32x4_t*>(yr + c * 8) = pack8(o);
     }
@@ -120,7 +138,7 @@ __global__ void modulation_kernel(const float* __restrict__ table, const float* 
 // built in float64 and rounded to fp32 on the host.
 // Work item: one wave per (token, tensor) with tensor 0 = q, 1 = k.
 // ---------------------------------------------------------------------------
-template <int GROUP_LANES>
+template <int GROUP_LANES, int NC>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     bf16_t* __restrict__ q, int64_t ldq, bf16_t* __restrict__ k, int64_t ldk, int T, int D,
     int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
@@ -135,77 +153,94 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   bf16_t* xr = which ? (k + (int64_t)row * ldk) : (q + (int64_t)row * ldq);
   const float* w = which ? wk : wq;
   const int nchunk = D >> 3;
-  float v[kMaxChunks][8];
-  float ss[kMaxChunks];
+  // Every load is issued before the reduction: the row (kept packed), the
+  // norm weights and, with RoPE, the table entries of the token's positions.
+  u32x4_t raw[NC];
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = i * 64 + lane;
-    ss[i] = 0.f;
-    if (c < nchunk) {
-      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(xr + c * 8);
-      unpack8(raw, v[i]);
+  for (int i = 0; i < NC; ++i) {
+    const int c = i * 64 + lane;
+    raw[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(xr + c * 8) : u32x4_t{0, 0, 0, 0};
+  }
+  f32x4_t w4[NC][2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss[i] = fmaf(v[i][j], v[i][j], ss[i]);
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(i * 64 + lane, nchunk - 1);
+    w4[i][0] = *reinterpret_cast<const f32x4_t*>(w + c * 8);
+    w4[i][1] = *reinterpret_cast<const f32x4_t*>(w + c * 8 + 4);
+  }
+  // RoPE: chunk c holds pairs p0..p0+3 of its head, p0 = 4 * (c % (head_dim/8));
+  // with 64 lanes per chunk row that is the same quad for every chunk of a lane,
+  // so each lane loads its rotation once.  The quad's pairs belong to at most
+  // two axes: table entries of the axis of the first pair and of the last pair.
+  const bool rope = rcos != nullptr;
+  const int p0 = (lane % (head_dim >> 3)) * 4;
+  float rc[4], rsn[4];
+  if (rope) {
+    const int half = head_dim >> 1;
+    const int seg = find_segment(cu, nseg, row);
+    const int s = row - cu[seg];
+    const int gh = grids[seg * 3 + 1], gw = grids[seg * 3 + 2];
+    const int pf = min(s / (gh * gw), max_pos - 1);
+    const int ph = min((s / gw) % gh, max_pos - 1);
+    const int pw = min(s % gw, max_pos - 1);
+    auto axis_pos = [&](int p) { return p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw); };
+    const int pa = axis_pos(p0), pb = axis_pos(p0 + 3);
+    const f32x4_t ca = *reinterpret_cast<const f32x4_t*>(rcos + pa * half + p0);
+    const f32x4_t sa = *reinterpret_cast<const f32x4_t*>(rsin + pa * half + p0);
+    f32x4_t cb = ca, sb = sa;
+    if (pb != pa) {
+      cb = *reinterpret_cast<const f32x4_t*>(rcos + pb * half + p0);
+      sb = *reinterpret_cast<const f32x4_t*>(rsin + pb * half + p0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool first = (p0 + j < t_pairs) == (p0 < t_pairs) &&
+                         (p0 + j < t_pairs + h_pairs) == (p0 < t_pairs + h_pairs);
+      rc[j] = first ? ca[j] : cb[j];
+      rsn[j] = first ? sa[j] : sb[j];
     }
   }
-  float rs[kMaxChunks];
-  if (GROUP_LANES == 64) {
-    float s = 0.f;
+  float rs[NC];
+  {
+    float ss[NC];
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) s += ss[i];
-    float r = rsqrtf(wave_sum<64>(s) / (float)D + eps);
+    for (int i = 0; i < NC; ++i) {
+      float v[8];
+      unpack8(raw[i], v);
+      ss[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) rs[i] = r;
-  } else {
-    // a head spans GROUP_LANES consecutive lanes of one chunk row
+      for (int j = 0; j < 8; ++j) ss[i] = fmaf(v[j], v[j], ss[i]);
+    }
+    if (GROUP_LANES == 64) {
+      float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i)
-      rs[i] = rsqrtf(wave_sum<GROUP_LANES>(ss[i]) / (float)head_dim + eps);
+      for (int i = 0; i < NC; ++i) t += ss[i];
+      const float r = rsqrtf(wave_sum<64>(t) / (float)D + eps);
+#pragma unroll
+      for (int i = 0; i < NC; ++i) rs[i] = r;
+    } else {
+      // a head spans GROUP_LANES consecutive lanes of one chunk row
+#pragma unroll
+      for (int i = 0; i < NC; ++i) rs[i] = rsqrtf(wave_sum<GROUP_LANES>(ss[i]) / (float)head_dim + eps);
+    }
   }
-  int pf = 0, ph = 0, pw = 0;
-  if (rcos != nullptr) {
-    int seg = find_segment(cu, nseg, row);
-    int s = row - cu[seg];
-    int gh = grids[seg * 3 + 1], gw = grids[seg * 3 + 2];
-    pf = s / (gh * gw);
-    ph = (s / gw) % gh;
-    pw = s % gw;
-    pf = min(pf, max_pos - 1);
-    ph = min(ph, max_pos - 1);
-    pw = min(pw, max_pos - 1);
-  }
-  const int half = head_dim >> 1;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    int c = i * 64 + lane;
+  for (int i = 0; i < NC; ++i) {
+    const int c = i * 64 + lane;
     if (c < nchunk) {
       float o[8];
-      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(w + c * 8);
-      const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(w + c * 8 + 4);
+      unpack8(raw[i], o);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        o[j] = v[i][j] * rs[i] * w0[j];
-        o[j + 4] = v[i][j + 4] * rs[i] * w1[j];
+        o[j] = o[j] * rs[i] * w4[i][0][j];
+        o[j + 4] = o[j + 4] * rs[i] * w4[i][1][j];
       }
-      if (rcos != nullptr) {
-        // pairs p0..p0+3 of this chunk; they belong to at most two axes, so
-        // read 16 bytes from the table row of the first and of the last pair.
-        const int p0 = ((c * 8) % head_dim) >> 1;
-        auto axis_pos = [&](int p) { return p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw); };
-        const int pa = axis_pos(p0), pb = axis_pos(p0 + 3);
-        const f32x4_t ca = *reinterpret_cast<const f32x4_t*>(rcos + pa * half + p0);
-        const f32x4_t sa = *reinterpret_cast<const f32x4_t*>(rsin + pa * half + p0);
-        const f32x4_t cb = *reinterpret_cast<const f32x4_t*>(rcos + pb * half + p0);
-        const f32x4_t sb = *reinterpret_cast<const f32x4_t*>(rsin + pb * half + p0);
+      if (rope) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const bool first = (p0 + j < t_pairs) == (p0 < t_pairs) &&
-                             (p0 + j < t_pairs + h_pairs) == (p0 < t_pairs + h_pairs);
-          const float cs = first ? ca[j] : cb[j];
-          const float sn = first ? sa[j] : sb[j];
           const float x1 = o[2 * j], x2 = o[2 * j + 1];
-          o[2 * j] = x1 * cs - x2 * sn;
-          o[2 * j + 1] = x1 * sn + x2 * cs;
+          o[2 * j] = x1 * rc[j] - x2 * rsn[j];
+          o[2 * j + 1] = x1 * rsn[j] + x2 * rc[j];
         }
       }
       *reinterpret_cast<u32x4_t*>(xr + c * 8) = pack8(o);
@@ -234,12 +269,28 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
   DITK_REQUIRE(norm_kind == 0 || norm_kind == 1, "ditk_adaln: norm_kind must be 0 (LN) or 1 (RMS)");
   if (T == 0) return 0;
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
-  if (norm_kind == 0)
-    adaln_kernel<0><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens,
-                                             nseg, shift, scale, mod_stride, weight, bias, eps);
-  else
-    adaln_kernel<1><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens,
-                                             nseg, shift, scale, mod_stride, weight, bias, eps);
+  const int nc = (D / 8 + 63) / 64;
+#define DITK_ADALN(K, NCV)                                                                            \
+  adaln_kernel<K, NCV><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens, \
+                                                 nseg, shift, scale, mod_stride, weight, bias, eps)
+#define DITK_ADALN_NC(K)              \
+  switch (nc) {                       \
+    case 1: DITK_ADALN(K, 1); break;  \
+    case 2: DITK_ADALN(K, 2); break;  \
+    case 3: DITK_ADALN(K, 3); break;  \
+    case 4: DITK_ADALN(K, 4); break;  \
+    case 5: DITK_ADALN(K, 5); break;  \
+    case 6: DITK_ADALN(K, 6); break;  \
+    case 7: DITK_ADALN(K, 7); break;  \
+    default: DITK_ADALN(K, 8); break; \
+  }
+  if (norm_kind == 0) {
+    DITK_ADALN_NC(0)
+  } else {
+    DITK_ADALN_NC(1)
+  }
+#undef DITK_ADALN_NC
+#undef DITK_ADALN
   return ditk_check_launch("ditk_adaln");
 }
 
@@ -273,13 +324,30 @@ DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, in
                "ditk_qk_norm_rope: RoPE tables must be 16-byte aligned");
   if (T == 0) return 0;
   dim3 grid((2 * T + kRowsPerBlock - 1) / kRowsPerBlock);
-#define DITK_QKN(G)                                                                             \
-  qk_norm_rope_kernel<G><<<grid, 256, 0, stream>>>((bf16_t*)q, ldq, (bf16_t*)k, ldk, T, D, head_dim, \
-                                                   wq, wk, eps, rope_cos, rope_sin, max_pos,    \
-                                                   cu_seqlens, grids, nseg, t_pairs, h_pairs)
-  if (!per_head) DITK_QKN(64);
-  else if (head_dim == 128) DITK_QKN(16);
-  else DITK_QKN(8);
+  const int nc = (D / 8 + 63) / 64;
+#define DITK_QKN(G, NCV)                                                                                  \
+  qk_norm_rope_kernel<G, NCV><<<grid, 256, 0, stream>>>((bf16_t*)q, ldq, (bf16_t*)k, ldk, T, D, head_dim, \
+                                                        wq, wk, eps, rope_cos, rope_sin, max_pos,         \
+                                                        cu_seqlens, grids, nseg, t_pairs, h_pairs)
+#define DITK_QKN_NC(G)              \
+  switch (nc) {                     \
+    case 1: DITK_QKN(G, 1); break;  \
+    case 2: DITK_QKN(G, 2); break;  \
+    case 3: DITK_QKN(G, 3); break;  \
+    case 4: DITK_QKN(G, 4); break;  \
+    case 5: DITK_QKN(G, 5); break;  \
+    case 6: DITK_QKN(G, 6); break;  \
+    case 7: DITK_QKN(G, 7); break;  \
+    default: DITK_QKN(G, 8); break; \
+  }
+  if (!per_head) {
+    DITK_QKN_NC(64)
+  } else if (head_dim == 128) {
+    DITK_QKN_NC(16)
+  } else {
+    DITK_QKN_NC(8)
+  }
+#undef DITK_QKN_NC
 #undef DITK_QKN
   return ditk_check_launch("ditk_qk_norm_rope");
 }

@@ -52,9 +52,19 @@ __device__ __forceinline__ int kperm(int m) {
 
 // 16 bytes per lane, global -> LDS; the 64 lanes of the wave fill 1 KiB of LDS
 // starting at the wave-uniform `lds_slot0` (lane l writes bytes l*16..l*16+15).
+// Issued as inline asm on purpose: the compiler then does not track the LDS
+// write, so it does not guard every later LDS read of *another* stage with a
+// full vmcnt(0) (it cannot tell the runtime stage indices apart, and that wait
+// would expose the prefetch's whole latency each tile).  The kernel orders the
+// DMA itself: each wave waits for its own DMA (dma_wait) before the barrier
+// that publishes a stage, and no stage is read before that barrier.
 __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
-                                   (__attribute__((address_space(3))) void*)lds_slot0, 16, 0, 0);
+  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)lds_slot0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gsrc), "s"(lds_addr)
+               : "memory", "m0");
 }
 
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -148,6 +158,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       if (qrow < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
       qf[qb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
+  // consume the Q loads here, so the compiler's own vmcnt wait for them sits
+  // before the key loop rather than at the first use inside it
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) asm volatile("" : "+v"(qf[qb][c]));
 
   f32x16_t o[QB][DT];
 #pragma unroll

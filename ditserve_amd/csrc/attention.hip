@@ -39,6 +39,9 @@ constexpr int BN = 64;   // keys per iteration
 #ifndef ATTN_QB
 #define ATTN_QB 1        // 32-query blocks per wave
 #endif
+#ifndef ATTN_ILV
+#define ATTN_ILV 1       // in-wave interleave of S(kt+1) MFMAs with P(kt) softmax (0: compiler order)
+#endif
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 constexpr float kRescaleSum = 256.0f;  // 2^kLazy: a lane's row sum above it triggers a rescale
 
@@ -377,6 +380,86 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     dma_wait();
     __syncthreads();
   }
+#if ATTN_ILV
+  // In-wave interleave: per 16-d chunk c of S(kt+1) = K(kt+1) Q^T, its MFMAs
+  // alternate with score pairs of P(kt) = exp2(S(kt) c - m) in a fixed issue
+  // order (sched_group_barrier), so the VALU work issues in the shadow of this
+  // wave's own MFMAs; K fragments are read one chunk ahead.  S(kt) and S(kt+1)
+  // alternate between two register sets (two tiles per trip).
+  auto steady_ilv = [&](int kt, f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2]) {
+    const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
+    if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);
+    issue_v(kt + 1, vcur ^ 1);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s_nxt[qb][kk][v] = 0.f;
+    uint32_t pf[QB][2][2][4];
+    float rs[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rs[qb] = 0.f;
+    constexpr int PAIRS = 16 * QB / (NC * 2);  // score pairs per MFMA slot (per kk half-chunk)
+    static_assert(PAIRS >= 1 && (16 * QB) % (NC * 2) == 0, "pair split");
+    auto pair = [&](int pi) {  // pair index over (qb, kk, j, e)
+      const int qb = pi / 16, r = pi % 16, kk = r >> 3, j = (r >> 2) & 1, e = r & 3;
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+      pf[qb][kk][j][e] = pack_bf2(p0, p1);
+      rs[qb] += p0 + p1;
+    };
+    bf16x8_t kf[2][2];
+    kf[0][0] = k_frag(knxt, 0, 0);
+    kf[0][1] = k_frag(knxt, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int cb = c & 1;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[cb][kk], qf[qb][c], s_nxt[qb][kk], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) pair((c * 2 + kk) * PAIRS + i);
+      }
+      if (c + 1 < NC) {
+        kf[cb ^ 1][0] = k_frag(knxt, c + 1, 0);
+        kf[cb ^ 1][1] = k_frag(knxt, c + 1, 1);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 7 * PAIRS, 0);
+      }
+      if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pin(pf);
+    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
+    pv(vcur, pf);
+    dma_wait();
+    __syncthreads();
+  };
+  {
+    f32x16_t (&sa)[QB][2] = s_next;
+    f32x16_t sb[QB][2];
+    int kt = 0;
+    for (; kt + 2 < nkt; kt += 2) {
+      steady_ilv(kt, sa, sb);
+      steady_ilv(kt + 1, sb, sa);
+    }
+    if (kt + 1 < nkt) {
+      steady_ilv(kt, sa, sb);
+      last(sb);
+    } else if (nkt > 0) {
+      last(sa);
+    }
+  }
+#else
   for (int kt = 0; kt + 1 < nkt; ++kt) {  // every tile but the last: all 64 keys valid
     const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
     if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);
@@ -395,6 +478,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     __syncthreads();
   }
   if (nkt > 0) last(s_next);
+#endif
 
   // ---- normalise and store
 #pragma unroll

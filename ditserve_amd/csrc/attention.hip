@@ -39,8 +39,14 @@ constexpr int BN = 64;   // keys per iteration
 #ifndef ATTN_QB
 #define ATTN_QB 1        // 32-query blocks per wave
 #endif
-#ifndef ATTN_ILV
-#define ATTN_ILV 1       // in-wave interleave of S(kt+1) MFMAs with P(kt) softmax (0: compiler order)
+#ifndef ATTN_SPLIT
+#define ATTN_SPLIT 1     // softmax pairs spread over both MFMA phases of a tile (0: compiler order)
+#endif
+#ifndef ATTN_KEARLY
+#define ATTN_KEARLY 1    // K fragments of chunk c+1 read right after chunk c's first MFMA
+#endif
+#ifndef ATTN_VAHEAD
+#define ATTN_VAHEAD 2    // Vt fragments in flight ahead of the PV MFMAs
 #endif
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 constexpr float kRescaleSum = 256.0f;  // 2^kLazy: a lane's row sum above it triggers a rescale
@@ -71,6 +77,17 @@ __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0
 }
 
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// sched_group_barrier of n VALU/TRANS instructions; n is a constant after
+// unrolling, the switch turns it into the literal the builtin needs
+__device__ __forceinline__ void valu_group(int n) {
+  switch (n) {
+#define VG(k) case k: __builtin_amdgcn_sched_group_barrier(0x402, k, 0); break;
+    VG(1) VG(2) VG(3) VG(4) VG(5) VG(6) VG(7) VG(8) VG(9) VG(10) VG(11) VG(12) VG(13) VG(14) VG(15) VG(16)
+#undef VG
+    default: break;
+  }
+}
 
 // segment m and tile index within it for the t-th (0-based) tile of `tile`-sized
 // tiles laid over the segments of cu; returns -1 if t is past the last tile.
@@ -104,8 +121,8 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 // plus a compile-time offset.
 // Per workgroup: NW waves x QB*32 queries of one (segment, head); per wave and
 // 64-key tile kt (steady state):
-//   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) = exp2(S(kt) c - m) on VALU
-//   B: O += Vt(kt) P(kt) on MFMA
+//   A: S(kt+1) = K(kt+1) Q^T on MFMA  ||  P(kt) keys 32..63 on VALU
+//   B: O += Vt(kt) P(kt) on MFMA      ||  P(kt+1) keys 0..31 on VALU
 // Each K / Vt fragment read from LDS feeds QB MFMAs (one per 32-query block).
 // K(kt) sits in LDS stage kt % KST (kept resident for the rescale path while
 // later tiles stream in), Vt(kt) in stage kt % 2.
@@ -304,9 +321,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int qb = 0; qb < QB; ++qb) r |= !(rs[qb] <= kRescaleSum);
     return __any(r);
   };
-  auto rescale_tile = [&](int kstage, uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
-    f32x16_t sr[QB][2];
-    compute_s(kstage, sr);
+  auto rescale_from = [&](const f32x16_t (&sr)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const float m_new = fmaxf(m_run[qb], row_max(sr[qb]));
@@ -319,6 +334,11 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
         for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
       rs[qb] = softmax_p(sr[qb], pf[qb], m_run[qb], valid);
     }
+  };
+  auto rescale_tile = [&](int kstage, uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
+    f32x16_t sr[QB][2];
+    compute_s(kstage, sr);
+    rescale_from(sr, pf, rs, valid);
   };
   auto pv = [&](int s, const uint32_t (&pf)[QB][2][2][4]) {
 #pragma unroll
@@ -359,15 +379,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     float rs[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s[qb], pf[qb], m_run[qb], valid);
-    if (needs_rescale(rs)) rescale_tile((nkt - 1) % KST, pf, rs, valid);
+    if (needs_rescale(rs)) rescale_from(s, pf, rs, valid);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
     pv((nkt - 1) & 1, pf);
   };
-  // Per tile: P(kt) on VALU, the (rare) rescale, S(kt+1) and PV(kt) on MFMA, in
-  // compiler order with one score register set; with two waves per SIMD one
-  // wave's MFMAs overlap the other's exp2.  K DMA runs two tiles ahead through
-  // three stages, Vt one tile ahead through two.
+  // K DMA runs two tiles ahead through three stages, Vt one tile ahead through two.
   if (nkt > 0) {
     issue_k(0, 0);
     dma_wait();
@@ -380,86 +397,175 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     dma_wait();
     __syncthreads();
   }
-#if ATTN_ILV
-  // In-wave interleave: per 16-d chunk c of S(kt+1) = K(kt+1) Q^T, its MFMAs
-  // alternate with score pairs of P(kt) = exp2(S(kt) c - m) in a fixed issue
-  // order (sched_group_barrier), so the VALU work issues in the shadow of this
-  // wave's own MFMAs; K fragments are read one chunk ahead.  S(kt) and S(kt+1)
-  // alternate between two register sets (two tiles per trip).
-  auto steady_ilv = [&](int kt, f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2]) {
-    const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
+#if ATTN_SPLIT
+  // Split interleave: the 16 score pairs of a tile are spread evenly over both
+  // MFMA phases of the wave.  Per tile kt:
+  //   phase 1: S(kt+1) = K(kt+1) Q^T   ||  P(kt) keys 32..63
+  //   (rescale check on keys 32..63)
+  //   phase 2: O += Vt(kt) P(kt)       ||  P(kt+1) keys 0..31
+  //   (rescale check on keys 0..31 of kt+1)
+  // The check of a half flags every half with a score above m + kLazy (its sum
+  // then exceeds 2^kLazy); the rescale raises m from the S registers still
+  // live, scales O and l, and recomputes the P values not yet folded into O.
+  auto pair_at = [&](const f32x16_t (&s)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int qb,
+                     int kk, int r) {
+    const int j = r >> 2, e = r & 3;
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+    pf[qb][kk][j][e] = pack_bf2(p0, p1);
+    rs[qb] += p0 + p1;
+  };
+  auto half_max = [&](const f32x16_t& sk) {
+    float a = sk[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) a = fmaxf(a, sk[v]);
+    return fmaxf(a, __shfl_xor(a, 32, 64)) * scale_log2;
+  };
+  auto raise_m = [&](int qb, float tile_max) {
+    const float m_new = fmaxf(m_run[qb], tile_max);
+    const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+    m_run[qb] = m_new;
+    l_run[qb] *= alpha;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
+  };
+  // ops of a pair: 2 fma, 2 exp2, 1 pack, 2 add
+  constexpr int POPS = 7;
+  auto steady_split = [&](int kt, f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2],
+                          uint32_t (&pf_cur)[QB][2][2][4], uint32_t (&pf_nxt)[QB][2][2][4],
+                          float (&rs0_cur)[QB], float (&rs0_nxt)[QB]) {
+    const int knxt = (kt + 1) % KST, vcur = kt & 1;
     if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);
     issue_v(kt + 1, vcur ^ 1);
+    float rs1[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s_nxt[qb][kk][v] = 0.f;
-    uint32_t pf[QB][2][2][4];
-    float rs[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = 0.f;
-    constexpr int PAIRS = 16 * QB / (NC * 2);  // score pairs per MFMA slot (per kk half-chunk)
-    static_assert(PAIRS >= 1 && (16 * QB) % (NC * 2) == 0, "pair split");
-    auto pair = [&](int pi) {  // pair index over (qb, kk, j, e)
-      const int qb = pi / 16, r = pi % 16, kk = r >> 3, j = (r >> 2) & 1, e = r & 3;
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
-      pf[qb][kk][j][e] = pack_bf2(p0, p1);
-      rs[qb] += p0 + p1;
-    };
-    bf16x8_t kf[2][2];
-    kf[0][0] = k_frag(knxt, 0, 0);
-    kf[0][1] = k_frag(knxt, 0, 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int cb = c & 1;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[cb][kk], qf[qb][c], s_nxt[qb][kk], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < PAIRS; ++i) pair((c * 2 + kk) * PAIRS + i);
-      }
-      if (c + 1 < NC) {
-        kf[cb ^ 1][0] = k_frag(knxt, c + 1, 0);
-        kf[cb ^ 1][1] = k_frag(knxt, c + 1, 1);
-      }
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, 7 * PAIRS, 0);
-      }
-      if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    for (int qb = 0; qb < QB; ++qb) rs1[qb] = 0.f;
+    // phase 1: 2*NC MFMA slots of QB MFMAs, 8*QB pairs of keys 32..63
+    {
+      constexpr int SLOTS = 2 * NC, OPS = POPS * 8 * QB;
+      bf16x8_t kf[2][2];
+      kf[0][0] = k_frag(knxt, 0, 0);
+      kf[0][1] = k_frag(knxt, 0, 1);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    pin(pf);
-    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
-    pv(vcur, pf);
+      for (int c = 0; c < NC; ++c) {
+        const int cb = c & 1;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int slot = c * 2 + kk;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                kf[cb][kk], qf[qb][c], c == 0 ? f32x16_t{} : s_nxt[qb][kk], 0, 0, 0);
+          // pairs whose first op falls in this slot
+#pragma unroll
+          for (int pi = 0; pi < 8 * QB; ++pi)
+            if ((pi * POPS * SLOTS) / OPS == slot) pair_at(s_cur, pf_cur, rs1, pi / 8, 1, pi % 8);
+        }
+        if (c + 1 < NC) {
+          kf[cb ^ 1][0] = k_frag(knxt, c + 1, 0);
+          kf[cb ^ 1][1] = k_frag(knxt, c + 1, 1);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int slot = c * 2 + kk;
+          __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+#if ATTN_KEARLY
+          if (kk == 0 && c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#endif
+          valu_group((OPS * (slot + 1)) / SLOTS - (OPS * slot) / SLOTS);
+        }
+#if !ATTN_KEARLY
+        if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    pin(pf_cur);
+    if (needs_rescale(rs1)) {
+      // P(kt) keys 0..31 are not in O yet either: the whole tile is redone from
+      // K(kt), still resident, so S(kt) keys 0..31 need not stay in registers
+      rescale_tile(kt % KST, pf_cur, rs1, BN);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) rs0_cur[qb] = 0.f;
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      l_run[qb] += rs0_cur[qb] + rs1[qb];
+      rs0_nxt[qb] = 0.f;
+    }
+    // phase 2: 4*DT MFMA slots (one Vt fragment, QB MFMAs each), 8*QB pairs of
+    // keys 0..31 of the next tile; Vt fragments read one slot ahead
+    {
+      constexpr int SLOTS = 4 * DT, OPS = POPS * 8 * QB;
+      constexpr int VA = ATTN_VAHEAD;  // Vt fragments in flight
+      bf16x8_t vb[VA + 1];
+#pragma unroll
+      for (int t = 0; t < VA; ++t) vb[t] = v_frag(vcur, t / DT, t % DT);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < SLOTS; ++t) {
+        const int g = t / DT, d = t % DT;
+        if (t + VA < SLOTS) vb[(t + VA) % (VA + 1)] = v_frag(vcur, (t + VA) / DT, (t + VA) % DT);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const uint32_t* p = pf_cur[qb][g >> 1][g & 1];
+          const u32x4_t p4 = u32x4_t{p[0], p[1], p[2], p[3]};
+          o[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb[t % (VA + 1)], __builtin_bit_cast(bf16x8_t, p4), o[qb][d], 0, 0, 0);
+        }
+#pragma unroll
+        for (int pi = 0; pi < 8 * QB; ++pi)
+          if ((pi * POPS * SLOTS) / OPS == t) pair_at(s_nxt, pf_nxt, rs0_nxt, pi / 8, 0, pi % 8);
+        if (t + VA < SLOTS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+        valu_group((OPS * (t + 1)) / SLOTS - (OPS * t) / SLOTS);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    pin(pf_nxt);
+    if (needs_rescale(rs0_nxt)) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        raise_m(qb, half_max(s_nxt[qb][0]));
+        rs0_nxt[qb] = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pair_at(s_nxt, pf_nxt, rs0_nxt, qb, 0, r);
+      }
+    }
     dma_wait();
     __syncthreads();
   };
   {
     f32x16_t (&sa)[QB][2] = s_next;
     f32x16_t sb[QB][2];
+    uint32_t pfa[QB][2][2][4], pfb[QB][2][2][4];
+    float rsa[QB], rsb[QB];
+    if (nkt > 1) {  // keys 0..31 of tile 0 against its exact max: no check needed
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        rsa[qb] = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pair_at(sa, pfa, rsa, qb, 0, r);
+      }
+    }
     int kt = 0;
     for (; kt + 2 < nkt; kt += 2) {
-      steady_ilv(kt, sa, sb);
-      steady_ilv(kt + 1, sb, sa);
+      steady_split(kt, sa, sb, pfa, pfb, rsa, rsb);
+      steady_split(kt + 1, sb, sa, pfb, pfa, rsb, rsa);
     }
+    // the last tile is redone from its scores with the key mask
     if (kt + 1 < nkt) {
-      steady_ilv(kt, sa, sb);
+      steady_split(kt, sa, sb, pfa, pfb, rsa, rsb);
       last(sb);
     } else if (nkt > 0) {
       last(sa);
     }
   }
 #else
+  // Compiler-ordered loop: P(kt), the (rare) rescale, then S(kt+1) and PV(kt);
+  // only the other wave of the SIMD overlaps softmax with MFMAs.
   for (int kt = 0; kt + 1 < nkt; ++kt) {  // every tile but the last: all 64 keys valid
     const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
     if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);

@@ -196,6 +196,29 @@ def test_attention_sharp_logits():
 
 
 @pytest.mark.parametrize("Dh", [128, 64])
+def test_attention_rising_scores(Dh):
+    """Scores rising by 0.3 per key (about 14 log2 units per 32 keys) for even query rows and
+    falling for odd ones: the running max has to be raised in every half tile, inside the key
+    loop and on each segment's last tile, while half the lanes of a wave keep their max."""
+    ops = _ops()
+    H, cu = 2, [0, 333, 1000, 1031]
+    T = cu[-1]
+    g = torch.Generator().manual_seed(80)
+    u = torch.randn(H, Dh, generator=g)
+    u = u / u.norm(dim=1, keepdim=True)
+    sign = torch.where(torch.arange(T) % 2 == 0, 1.0, -1.0)
+    q = (math.sqrt(Dh) * sign[:, None, None] * u[None]).expand(T, H, Dh)
+    pos = torch.cat([torch.arange(cu[m + 1] - cu[m], dtype=torch.float32) for m in range(len(cu) - 1)])
+    k = 0.3 * pos[:, None, None] * u[None] + 0.1 * torch.randn(T, H, Dh, generator=g)
+    v = torch.randn(T, H, Dh, generator=g)
+    q, k, v = (bf(t.reshape(T, H * Dh)) for t in (q, k, v))
+    seg = _seg(cu)
+    out = ops.flash_attn_varlen(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), v.to(DEV, torch.bfloat16),
+                                seg, seg, H, Dh).float().cpu()
+    assert_close(out, _attn_ref(q, k, v, cu, cu, H, Dh), cos_min=0.9999, rel_max=1e-2, label=f"rising Dh={Dh}")
+
+
+@pytest.mark.parametrize("Dh", [128, 64])
 def test_cross_attention_text_blocks(Dh):
     ops = _ops()
     H = 4

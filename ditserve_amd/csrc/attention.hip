@@ -415,6 +415,45 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     pf[qb][kk][j][e] = pack_bf2(p0, p1);
     rs[qb] += p0 + p1;
   };
+  // A pair is issued in two halves: (2 fma, 2 exp2) and (pack, 2 add), in the
+  // item order a0 a1 b0 a2 b1 ... a(n-1) b(n-2) b(n-1), so MFMAs sit between
+  // each exp2 and its first use instead of a wait.
+  auto item = [](int k, int n, int& pi) {  // 0: exp half of pair pi, 1: pack half
+    if (k == 0) { pi = 0; return 0; }
+    if (k == 2 * n - 1) { pi = n - 1; return 1; }
+    if (k & 1) { pi = (k + 1) / 2; return 0; }
+    pi = k / 2 - 1;
+    return 1;
+  };
+  auto pair_a = [&](const f32x16_t (&s)[QB][2], float (&ph)[2], int qb, int kk, int r) {
+    const int j = r >> 2, e = r & 3;
+    ph[0] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+    ph[1] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+  };
+  auto pair_b = [&](uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], const float (&ph)[2], int qb, int kk, int r) {
+    pf[qb][kk][r >> 2][r & 3] = pack_bf2(ph[0], ph[1]);
+    rs[qb] += ph[0] + ph[1];
+  };
+  // the items of slot t (of `slots`) over n pairs, and their VALU op count
+  auto slot_items = [&](int t, int slots, int n, const f32x16_t (&s)[QB][2], uint32_t (&pf)[QB][2][2][4],
+                        float (&rs)[QB], float (&ph)[8 * QB][2], int kk) {
+#pragma unroll
+    for (int k = 0; k < 2 * n; ++k)
+      if ((k * slots) / (2 * n) == t) {
+        int pi;
+        if (item(k, n, pi) == 0) pair_a(s, ph[pi], pi / 8, kk, pi % 8);
+        else pair_b(pf, rs, ph[pi], pi / 8, kk, pi % 8);
+      }
+  };
+  auto slot_ops = [&](int t, int slots, int n) {
+    int ops = 0;
+    for (int k = 0; k < 2 * n; ++k)
+      if ((k * slots) / (2 * n) == t) {
+        int pi;
+        ops += item(k, n, pi) == 0 ? 4 : 3;
+      }
+    return ops;
+  };
   auto half_max = [&](const f32x16_t& sk) {
     float a = sk[0];
 #pragma unroll
@@ -431,8 +470,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
   };
-  // ops of a pair: 2 fma, 2 exp2, 1 pack, 2 add
-  constexpr int POPS = 7;
   auto steady_split = [&](int kt, f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2],
                           uint32_t (&pf_cur)[QB][2][2][4], uint32_t (&pf_nxt)[QB][2][2][4],
                           float (&rs0_cur)[QB], float (&rs0_nxt)[QB]) {
@@ -444,7 +481,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int qb = 0; qb < QB; ++qb) rs1[qb] = 0.f;
     // phase 1: 2*NC MFMA slots of QB MFMAs, 8*QB pairs of keys 32..63
     {
-      constexpr int SLOTS = 2 * NC, OPS = POPS * 8 * QB;
+      constexpr int SLOTS = 2 * NC;
+      float ph1[8 * QB][2];
       bf16x8_t kf[2][2];
       kf[0][0] = k_frag(knxt, 0, 0);
       kf[0][1] = k_frag(knxt, 0, 1);
@@ -459,10 +497,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
           for (int qb = 0; qb < QB; ++qb)
             s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 kf[cb][kk], qf[qb][c], c == 0 ? f32x16_t{} : s_nxt[qb][kk], 0, 0, 0);
-          // pairs whose first op falls in this slot
-#pragma unroll
-          for (int pi = 0; pi < 8 * QB; ++pi)
-            if ((pi * POPS * SLOTS) / OPS == slot) pair_at(s_cur, pf_cur, rs1, pi / 8, 1, pi % 8);
+          slot_items(slot, SLOTS, 8 * QB, s_cur, pf_cur, rs1, ph1, 1);
         }
         if (c + 1 < NC) {
           kf[cb ^ 1][0] = k_frag(knxt, c + 1, 0);
@@ -475,7 +510,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
 #if ATTN_KEARLY
           if (kk == 0 && c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #endif
-          valu_group((OPS * (slot + 1)) / SLOTS - (OPS * slot) / SLOTS);
+          valu_group(slot_ops(slot, SLOTS, 8 * QB));
         }
 #if !ATTN_KEARLY
         if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
@@ -499,7 +534,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     // phase 2: 4*DT MFMA slots (one Vt fragment, QB MFMAs each), 8*QB pairs of
     // keys 0..31 of the next tile; Vt fragments read one slot ahead
     {
-      constexpr int SLOTS = 4 * DT, OPS = POPS * 8 * QB;
+      constexpr int SLOTS = 4 * DT;
+      float ph2[8 * QB][2];
       constexpr int VA = ATTN_VAHEAD;  // Vt fragments in flight
       bf16x8_t vb[VA + 1];
 #pragma unroll
@@ -515,12 +551,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
           const u32x4_t p4 = u32x4_t{p[0], p[1], p[2], p[3]};
           o[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb[t % (VA + 1)], __builtin_bit_cast(bf16x8_t, p4), o[qb][d], 0, 0, 0);
         }
-#pragma unroll
-        for (int pi = 0; pi < 8 * QB; ++pi)
-          if ((pi * POPS * SLOTS) / OPS == t) pair_at(s_nxt, pf_nxt, rs0_nxt, pi / 8, 0, pi % 8);
+        slot_items(t, SLOTS, 8 * QB, s_nxt, pf_nxt, rs0_nxt, ph2, 0);
         if (t + VA < SLOTS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-        valu_group((OPS * (t + 1)) / SLOTS - (OPS * t) / SLOTS);
+        valu_group(slot_ops(t, SLOTS, 8 * QB));
         __builtin_amdgcn_sched_barrier(0);
       }
     }

@@ -67,13 +67,13 @@ __device__ __forceinline__ int kperm(int m) {
 // would expose the prefetch's whole latency each tile).  The kernel orders the
 // DMA itself: each wave waits for its own DMA (dma_wait) before the barrier
 // that publishes a stage, and no stage is read before that barrier.
+// The LDS address goes in M0 through the "{m0}" operand, so the compiler sets
+// M0 itself and knows it is used; the s_nop is the wait state an M0 write needs
+// before an LDS DMA reads it.
 __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0) {
   const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)lds_slot0);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(gsrc), "s"(lds_addr)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(lds_addr) : "memory");
 }
 
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -5,30 +5,22 @@
 // A is the token-major activation [M, K]; W is an nn.Linear weight [N, K]; both
 // are K-contiguous, which is what the MFMA operands want (each lane feeds 8
 // consecutive k values).  The kernel computes C^T tiles: the MFMA "A" operand
-// is a 32-row slice of W and the "B" operand a 32-token slice of the
+// is a 16-row slice of W and the "B" operand a 16-token slice of the
 // activation, so every lane ends up owning one token and 4 consecutive output
-// features per accumulator group -> 8-byte row-major stores.
+// features per accumulator tile -> 8-byte row-major staging writes.
 //
-// Tiling (gfx950, v_mfma_f32_32x32x16_bf16): a 512-thread workgroup computes a
-// 256 (tokens) x 256 (features) tile as 2 x 4 waves of 128 tokens x 64
-// features (8 accumulator tiles per wave), two waves per SIMD so one wave's
-// MFMAs issue while the other waits to issue its DMA.  K advances through
-// 128 KiB of LDS stages filled by direct global->LDS DMA (no register
-// staging): two stages of 64 k when K % 64 == 0, else four of 32 k.  The bias
-// is loaded before the k loop, so the epilogue of a bias / GELU / SiLU
-// projection waits on no global load.
+// Tiling (gfx950, v_mfma_f32_16x16x32_bf16, which draws less power per FLOP
+// than the 32x32x16 form): a 512-thread workgroup computes a 256 (tokens) x 256
+// (features) tile as 2 x 4 waves of 128 tokens x 64 features (4 x 8
+// accumulator tiles of 16 x 16 per wave), two waves per SIMD so one wave's
+// MFMAs issue while the other waits on its DMA or LDS reads.  K advances
+// through 128 KiB of LDS stages filled by direct global->LDS DMA (no register
+// staging): two stages of 64 k when K % 64 == 0, else four of 32 k.
 //
 // The k-loop order is fixed and there is no split-K, so every output element is
 // computed the same way whatever M is and wherever its row sits: packed and
 // per-request projections agree bitwise.
 #include "ditk_common.h"
-
-#ifndef GEMM_WAVES
-#define GEMM_WAVES 8  // waves per workgroup (4: one per SIMD, 8: two per SIMD)
-#endif
-#ifndef GEMM_BIAS_EARLY
-#define GEMM_BIAS_EARLY (GEMM_WAVES == 8)  // bias loaded before the k loop
-#endif
 
 namespace {
 
@@ -43,23 +35,22 @@ enum Epilogue : int {
 
 constexpr int GBM = 256;                     // tokens per workgroup tile
 constexpr int GBN = 256;                     // features per workgroup tile
-constexpr int GW = GEMM_WAVES;               // waves per workgroup: 2 x (GW/2) wave tiles
+constexpr int GW = 8;                        // waves per workgroup: 2 x (GW/2) wave tiles
 constexpr int WTM = GBM / 2;                 // tokens per wave tile
 constexpr int WTN = GBN / (GW / 2);          // features per wave tile
-constexpr int NI = WTN / 32, NJ = WTM / 32;  // 32x32 MFMA tiles per wave tile
 constexpr int LDS_STAGE_BYTES = 128 * 1024;  // k stages (reused by the epilogue staging)
 
 // k-stage geometry for BK k values per stage (BK = 64 when K allows, else 32)
 template <int BK>
 struct Stages {
   static constexpr int GBK = BK;
-  static constexpr int NCH = BK / 16;                 // 16-k MFMA chunks per stage
+  static constexpr int NCH = BK / 32;                 // 32-k MFMA chunks per stage
   static constexpr int CPRW = BK / 8;                 // 16-byte chunks per LDS row
   static constexpr int RPG = 64 / CPRW;               // rows filled by one DMA instruction (1 KiB)
   static constexpr int NGRP = GBM / RPG;              // DMA instructions per operand and stage
   static constexpr int NSTAGE = LDS_STAGE_BYTES / ((GBM + GBN) * BK * 2);
   static constexpr int DPW = NGRP / GW;               // DMA instructions per operand, wave and stage
-  static_assert(GBM == GBN && (BK == 32 || BK == 64) && NSTAGE >= 2 && NCH % 2 == 0, "tile configuration");
+  static_assert(GBM == GBN && (BK == 32 || BK == 64) && NSTAGE >= 2, "tile configuration");
   // LDS stage layout (A and W alike): row r of BK k-values = CPRW chunks of
   // 16 B, slot(r, u) = r*CPRW + (u ^ swz(r)).  A DMA instruction fills 64
   // contiguous slots (RPG whole rows); 16 consecutive lanes reading chunk u of
@@ -82,6 +73,12 @@ __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
                                    (__attribute__((address_space(3))) void*)lds_slot0, 16, 0, 0);
 }
+// Per 32 k a wave reads 4 feature fragments (double-buffered) and 8 token
+// fragments (single-buffered: token fragment j of the next chunk is read right
+// after the 4 MFMAs that use fragment j of this one).  Accumulator lane layout:
+// features f = i*16 + 4*(lane/16) + e, token t = j*16 + lane % 16 of the wave
+// tile.  The bias is loaded after the k loop (holding it through the loop would
+// spill).
 template <int EPI, int BK>
 __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
@@ -89,16 +86,13 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n) {
   using S = Stages<BK>;
-  constexpr int GBK = S::GBK, NCH = S::NCH, CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW = S::DPW;
-  // 128 KiB of LDS: NSTAGE stages of A and W tiles; reused by the epilogue as
-  // one [WTM tokens][WTN features] bf16 staging tile per wave.
+  constexpr int CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW = S::DPW;
+  constexpr int NCH = S::NCH;
+  constexpr int FI = WTN / 16, FJ = WTM / 16;  // feature / token fragments per wave (4, 8)
   __shared__ u32x4_t lds[NSTAGE * (GBM + GBN) * CPRW];
   auto As = [&](int s) { return lds + s * (GBM * CPRW); };
   auto Ws = [&](int s) { return lds + NSTAGE * GBM * CPRW + s * (GBN * CPRW); };
 
-  // XCD-aware grouped tile order: the 8 XCDs receive workgroup ids round-robin;
-  // give each XCD a contiguous run of logical tiles, ordered in groups of
-  // GROUP_M m-tiles so concurrently running tiles share A rows and W rows in L2.
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (b & 7) * (nb >> 3) + (b >> 3);
   if (L >= tiles_m * tiles_n) return;
@@ -110,190 +104,157 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   const int m0 = mt * GBM, n0 = nt * GBN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int ql = lane & 15, g = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const int wm = wave_u & 1, wn = wave_u >> 1;  // wave tile: tokens wm*WTM.., features wn*WTN..
+  const int wm = wave_u & 1, wn = wave_u >> 1;
+  const int a_row0 = wm * WTM, w_row0 = wn * WTN;
 
-  // ---- DMA source offsets (elements, per lane, loop invariant).  Group g of
-  // 64 slots covers rows RPG*g ..; lane l -> row RPG*g + l/CPRW, stored chunk
-  // l%CPRW, k chunk (l%CPRW) ^ swz(row).  Rows past M / N re-read the last row.
   const bf16_t* Ablk = A + (int64_t)m0 * lda;
   const bf16_t* Wblk = W + (int64_t)n0 * ldw;
-  uint32_t a_off[DPW], w_off[DPW];  // element offsets within the workgroup's row block
+  uint32_t a_off[DPW], w_off[DPW];
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {
-    const int g = i * GW + wave_u;
-    const int row = g * RPG + lane / CPRW;
+    const int gi = i * GW + wave_u;
+    const int row = gi * RPG + lane / CPRW;
     const int ksw = ((lane % CPRW) ^ S::swz(row)) * 8;
     a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + ksw);
     w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + ksw);
   }
-  // DMA instruction d (0 .. 2*DPW-1) of stage kt: even d -> A, odd d -> W
   auto dma_one = [&](int kt, int d) {
-    const int s = kt % NSTAGE, i = d >> 1, g = i * GW + wave_u;
-    if ((d & 1) == 0) lds_dma16(Ablk + kt * GBK + a_off[i], &As(s)[g * 64]);
-    else lds_dma16(Wblk + kt * GBK + w_off[i], &Ws(s)[g * 64]);
+    const int s = kt % NSTAGE, i = d >> 1, gi = i * GW + wave_u;
+    if ((d & 1) == 0) lds_dma16(Ablk + kt * BK + a_off[i], &As(s)[gi * 64]);
+    else lds_dma16(Wblk + kt * BK + w_off[i], &Ws(s)[gi * 64]);
   };
   auto issue = [&](int kt) {
 #pragma unroll
     for (int d = 0; d < 2 * DPW; ++d) dma_one(kt, d);
   };
 
-  // ---- operand read bases: row 32t + l32, k chunk c*2 + hh of MFMA chunk c
+  // operand read base of chunk c: row x*16 + ql, 16-byte chunk c*4 + g (the
+  // stage swizzle of row x*16 + ql depends on ql only)
   int rbase[NCH];
-  {
-    const int sg = S::swz(l32);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) rbase[c] = l32 * CPRW + ((c * 2 + hh) ^ sg);
-  }
-  const int a_row0 = wm * WTM, w_row0 = wn * WTN;
+  for (int c = 0; c < NCH; ++c) rbase[c] = ql * CPRW + ((c * 4 + g) ^ S::swz(ql));
 
-  // bias of the lane's accumulator features f = i*32 + gq*8 + hh*4 .. +3
-  // (columns past N read the last valid group and are never stored)
-  f32x4_t bvec[NI][4];
+  f32x4_t bvec[FI];
   auto load_bias = [&]() {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
-        bvec[i][gq] = bias != nullptr
-                          ? *reinterpret_cast<const f32x4_t*>(bias + min(n0 + w_row0 + i * 32 + gq * 8 + hh * 4, N - 4))
-                          : f32x4_t{0.f, 0.f, 0.f, 0.f};
-  };
-  if (GEMM_BIAS_EARLY) load_bias();
-
-  f32x16_t acc[NI][NJ];  // [feature tile i][token tile j]
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nk = K / GBK;
-  auto read_chunk = [&](int s, int c, bf16x8_t (&af)[NI], bf16x8_t (&bf)[NJ]) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) af[i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + i * 32) * CPRW]);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) bf[j] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + j * 32) * CPRW]);
-  };
-  // operand read r (0 .. NI+NJ-1) of chunk c from stage s into (af, bf)
-  auto read_one = [&](int s, int c, int r, bf16x8_t (&af)[NI], bf16x8_t (&bf)[NJ]) {
-    if (r < NI) af[r] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + r * 32) * CPRW]);
-    else bf[r - NI] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + (r - NI) * 32) * CPRW]);
+    for (int i = 0; i < FI; ++i)
+      bvec[i] = bias != nullptr ? *reinterpret_cast<const f32x4_t*>(bias + min(n0 + w_row0 + i * 16 + 4 * g, N - 4))
+                                : f32x4_t{0.f, 0.f, 0.f, 0.f};
   };
 
-  // Pipeline over k stages (NCH chunks of 16 k each).  Iteration kt: part A
-  // runs the MFMAs of chunks 0..NCH-2 while reading chunks 1..NCH-1; then this
-  // wave waits for its DMA of stage kt+1 and a barrier publishes that stage and
-  // frees buffer kt (all its operand reads are in registers); part B runs chunk
-  // NCH-1's MFMAs while reading chunk 0 of stage kt+1 and issuing the DMA of
-  // stage kt+NSTAGE into the freed buffer.  A plain s_barrier (no release fence,
-  // which would drain every stage in flight) suffices because each wave waits
-  // for its own DMA with vmcnt first.  MFMAs, operand reads and DMA issues are
-  // interleaved in groups fenced by sched_barrier.
+  f32x4_t acc[FI][FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / BK;
+  bf16x8_t fw[2][FI], fx[FJ];
+  auto read_w = [&](int s, int c, int i, bf16x8_t (&dst)[FI]) {
+    dst[i] = __builtin_bit_cast(bf16x8_t, Ws(s)[rbase[c] + (w_row0 + i * 16) * CPRW]);
+  };
+  auto read_x = [&](int s, int c, int j) {
+    fx[j] = __builtin_bit_cast(bf16x8_t, As(s)[rbase[c] + (a_row0 + j * 16) * CPRW]);
+  };
 #pragma unroll
   for (int kt = 0; kt < NSTAGE; ++kt)
     if (kt < nk) issue(kt);
-  bf16x8_t fa[2][NI], fb[2][NJ];
   S::dma_wait(min(NSTAGE - 1, nk - 1));
   __syncthreads();
-  read_chunk(0, 0, fa[0], fb[0]);
+#pragma unroll
+  for (int i = 0; i < FI; ++i) read_w(0, 0, i, fw[0]);
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) read_x(0, 0, j);
 
   auto publish = [&]() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
   };
-  constexpr int NM = NI * NJ;  // MFMAs per chunk
-  constexpr int NR = NI + NJ;  // operand reads per chunk
-  constexpr int NQ = NM / 2;   // groups of 2 MFMAs per chunk
-  constexpr int RPQ = (NR + NQ - 1) / NQ;           // operand reads per group
-  constexpr int DPQ = (2 * DPW + NQ - 1) / NQ;      // DMA issues per group of part B
-  // one interleave group: 2 MFMAs of the current chunk (operand set p), reads of chunk cn of
-  // stage sn into set p^1, DMA issues d0.. of stage kd
-  auto step = [&](int q, int p, int sn, int cn, int kd, bool reads, bool dmas) {
-    const int x0 = 2 * q, i0 = x0 / NJ, j0 = x0 % NJ;
-    acc[i0][j0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][i0], fb[p][j0], acc[i0][j0], 0, 0, 0);
-    acc[i0][j0 + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][i0], fb[p][j0 + 1], acc[i0][j0 + 1], 0, 0, 0);
+  // group j of a chunk (operand set p for the feature fragments): the 4 MFMAs of
+  // token fragment j, then the reads of the next chunk (cn of stage sn): token
+  // fragment j into fx[j] and, every other group, a feature fragment into set p^1;
+  // and DMA issue j of stage kd
+  auto step = [&](int j, int p, int sn, int cn, int kd, bool reads, bool dmas) {
+#pragma unroll
+    for (int i = 0; i < FI; ++i)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[p][i], fx[j], acc[i][j], 0, 0, 0);
     if (reads) {
-#pragma unroll
-      for (int r = q * RPQ; r < q * RPQ + RPQ; ++r)
-        if (r < NR) read_one(sn, cn, r, fa[p ^ 1], fb[p ^ 1]);
+      read_x(sn, cn, j);
+      if (j % 2 == 1) read_w(sn, cn, j / 2, fw[p ^ 1]);
     }
-    if (dmas) {
-#pragma unroll
-      for (int d = q * DPQ; d < q * DPQ + DPQ; ++d)
-        if (d < 2 * DPW) dma_one(kd, d);
-    }
+    if (dmas && j < 2 * DPW) dma_one(kd, j);
     __builtin_amdgcn_sched_barrier(0);
   };
+  static_assert(FJ == 2 * FI && 2 * DPW <= FJ && (NCH % 2 == 0 || NCH == 1), "group layout");
+  // with one chunk per stage the next stage's feature fragments land in set 1:
+  // swap the two sets after each stage (4 fragments, only the 32-k stage path)
+  auto rotate = [&]() {
+    if (NCH % 2 == 1) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+        const bf16x8_t t = fw[0][i];
+        fw[0][i] = fw[1][i];
+        fw[1][i] = t;
+      }
+    }
+  };
   int kt = 0;
-  // steady state: every stage has a successor and a DMA to issue
   for (; kt + NSTAGE < nk; ++kt) {
     const int s = kt % NSTAGE;
 #pragma unroll
     for (int c = 0; c + 1 < NCH; ++c)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) step(q, c & 1, s, c + 1, 0, true, false);
-    S::dma_wait(NSTAGE - 2);  // stage kt+1 landed (this wave)
+      for (int j = 0; j < FJ; ++j) step(j, c & 1, s, c + 1, 0, true, false);
+    S::dma_wait(NSTAGE - 2);
     publish();
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) step(q, 1, (kt + 1) % NSTAGE, 0, kt + NSTAGE, true, true);
+    for (int j = 0; j < FJ; ++j) step(j, (NCH - 1) & 1, (kt + 1) % NSTAGE, 0, kt + NSTAGE, true, true);
+    rotate();
   }
-  // drain: no more DMA to issue
   for (; kt < nk; ++kt) {
     const int s = kt % NSTAGE;
 #pragma unroll
     for (int c = 0; c + 1 < NCH; ++c)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) step(q, c & 1, s, c + 1, 0, true, false);
+      for (int j = 0; j < FJ; ++j) step(j, c & 1, s, c + 1, 0, true, false);
     const bool next = kt + 1 < nk;
     if (next) {
       S::dma_wait(nk - 2 - kt);
       publish();
     }
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) step(q, 1, (kt + 1) % NSTAGE, 0, 0, next, false);
+    for (int j = 0; j < FJ; ++j) step(j, (NCH - 1) & 1, (kt + 1) % NSTAGE, 0, 0, next, false);
+    rotate();
   }
   __syncthreads();
+  load_bias();
 
-  // ---------------------------------------------------------------- epilogue
-  if (!GEMM_BIAS_EARLY) load_bias();
-  // Accumulator lane layout: token t = j*32 + l32 of the wave tile, features
-  // f = i*32 + g*8 + hh*4 + e.
   if (EPI == EPI_F32) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int m = m0 + a_row0 + j * 32 + l32;
+    for (int j = 0; j < FJ; ++j) {
+      const int m = m0 + a_row0 + j * 16 + ql;
       if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int n = n0 + w_row0 + i * 32 + gq * 8 + hh * 4;
-          if (n >= N) continue;
-          float o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = acc[i][j][gq * 4 + e] + bvec[i][gq][e];
-          float* C = reinterpret_cast<float*>(Cv) + (int64_t)m * ldc + n;
-          *reinterpret_cast<f32x4_t*>(C) = f32x4_t{o[0], o[1], o[2], o[3]};
-        }
+      for (int i = 0; i < FI; ++i) {
+        const int n = n0 + w_row0 + i * 16 + 4 * g;
+        if (n >= N) continue;
+        *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(Cv) + (int64_t)m * ldc + n) = acc[i][j] + bvec[i];
+      }
     }
     return;
   }
-  // bf16 epilogues: y = bf16(acc + bias) goes through a per-wave LDS tile
-  // [WTM tokens][WTN features] (16-byte chunk c of row t stored at c ^ (t % CPR)),
-  // then rows are read back so residual / gate loads and output stores are
-  // 16-byte coalesced.  Lane (c, row group) handles features n..n+7 of rows
-  // t = r*RPP + lane/CPR; its residual rows and gate are loaded before the
-  // staging, so their latency overlaps it instead of stalling each row.
-  constexpr int CPR = WTN / 8;   // 16-byte chunks per staged row
-  constexpr int RPP = 64 / CPR;  // rows per pass of the wave
-  constexpr int NPASS = WTM / RPP;  // passes
+  // bf16 epilogues through a per-wave LDS tile [WTM tokens][WTN features]: 8-byte
+  // unit u (features 4u..4u+3) of row t stored at u ^ (2 * ((t >> 1) & 7)), so the
+  // 16 rows of one write hit distinct banks and 16-byte unit pairs stay together.
+  constexpr int CPR = WTN / 8;
+  constexpr int RPP = 64 / CPR;
+  constexpr int NPASS = WTM / RPP;
   constexpr bool HAS_RES = EPI == EPI_GATE_RES || EPI == EPI_RES;
-  const int c = lane % CPR;
-  const int n = n0 + w_row0 + c * 8;
-  const int mrow = m0 + a_row0 + lane / CPR;  // row of pass 0; pass r adds r*RPP
+  const int c8 = lane % CPR;
+  const int n = n0 + w_row0 + c8 * 8;
+  const int mrow = m0 + a_row0 + lane / CPR;
   u32x4_t res[HAS_RES ? NPASS : 1];
   if (HAS_RES) {
 #pragma unroll
@@ -302,8 +263,6 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
       res[r] = (m < M && n < N) ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
     }
   }
-  // gate rows: one segment for the whole wave tile (the common case) loads its
-  // gate once; a tile that straddles a segment boundary looks it up per row
   int seg_lo = 0;
   bool one_seg = true;
   f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
@@ -311,27 +270,21 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     seg_lo = find_segment(cu, nseg, m0 + a_row0);
     one_seg = seg_lo == find_segment(cu, nseg, min(m0 + a_row0 + WTM, M) - 1);
     if (one_seg && n < N) {
-      const float* g = gate + (int64_t)seg_lo * gate_stride + n;
-      g0 = *reinterpret_cast<const f32x4_t*>(g);
-      g1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+      const float* gp = gate + (int64_t)seg_lo * gate_stride + n;
+      g0 = *reinterpret_cast<const f32x4_t*>(gp);
+      g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
     }
   }
   u32x2_t* stage8 = reinterpret_cast<u32x2_t*>(lds + wave_u * (WTM * CPR));
   const u32x4_t* stage16 = lds + wave_u * (WTM * CPR);
-  static_assert(NSTAGE * (GBM + GBN) * CPRW >= GW * WTM * CPR, "epilogue staging exceeds the LDS stages");
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4_t b4 = bvec[i][gq];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int t = j * 32 + l32;
-        const int chunk = (i * 4 + gq) ^ (t % CPR);
-        stage8[(t * CPR + chunk) * 2 + hh] =
-            u32x2_t{pack_bf2(acc[i][j][gq * 4 + 0] + b4[0], acc[i][j][gq * 4 + 1] + b4[1]),
-                    pack_bf2(acc[i][j][gq * 4 + 2] + b4[2], acc[i][j][gq * 4 + 3] + b4[3])};
-      }
+    for (int j = 0; j < FJ; ++j) {
+      const int t = j * 16 + ql;
+      const int u = (i * 4 + g) ^ (2 * ((t >> 1) & 7));
+      const f32x4_t y = acc[i][j] + bvec[i];
+      stage8[t * (2 * CPR) + u] = u32x2_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
     }
   __syncthreads();
   if (n >= N) return;
@@ -340,7 +293,7 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     const int t = r * RPP + lane / CPR;
     const int m = mrow + r * RPP;
     if (m >= M) continue;
-    u32x4_t v = stage16[t * CPR + (c ^ (t % CPR))];
+    u32x4_t v = stage16[t * CPR + (c8 ^ ((t >> 1) & 7))];
     if (EPI != EPI_BIAS) {
       float x[8];
       unpack8(v, x);
@@ -356,9 +309,9 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
         if (EPI == EPI_GATE_RES) {
           f32x4_t h0 = g0, h1 = g1;
           if (!one_seg) {
-            const float* g = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
-            h0 = *reinterpret_cast<const f32x4_t*>(g);
-            h1 = *reinterpret_cast<const f32x4_t*>(g + 4);
+            const float* gp = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+            h0 = *reinterpret_cast<const f32x4_t*>(gp);
+            h1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {

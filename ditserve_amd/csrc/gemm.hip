@@ -65,7 +65,12 @@ struct Stages {
   }
 };
 
-constexpr int GROUP_M = 8;  // m-tiles per tile-order group (L2 reuse of W)
+// Tile order: groups of `group_m` m-tiles walked m-fastest within the group, so
+// the tiles running together share A rows and W rows in L2.  Chosen per shape
+// (measured on the block GEMMs, same box): long K favours narrow groups
+// (ffn-down: 1.39 ms at 1 vs 1.46 at 8), many n-tiles favour 4 (ffn-up: 1.58 vs
+// 1.73), the rest 8.  The order does not change any result.
+int gemm_group_m(int K, int tiles_n) { return K >= 4096 ? 1 : (tiles_n >= 24 ? 4 : 8); }
 
 // 16 bytes per lane, global -> LDS; the wave's 64 lanes fill 1 KiB starting at
 // the wave-uniform lds_slot0 (lane l writes bytes 16l .. 16l+15).
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
-    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n) {
+    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
   using S = Stages<BK>;
   constexpr int CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW = S::DPW;
   constexpr int NCH = S::NCH;
@@ -96,10 +101,10 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (b & 7) * (nb >> 3) + (b >> 3);
   if (L >= tiles_m * tiles_n) return;
-  const int group = L / (GROUP_M * tiles_n);
-  const int first_m = group * GROUP_M;
-  const int gm = min(GROUP_M, tiles_m - first_m);
-  const int pid = L % (GROUP_M * tiles_n);
+  const int group = L / (group_m * tiles_n);
+  const int first_m = group * group_m;
+  const int gm = min(group_m, tiles_m - first_m);
+  const int pid = L % (group_m * tiles_n);
   const int mt = first_m + pid % gm, nt = pid / gm;
   const int m0 = mt * GBM, n0 = nt * GBN;
 
@@ -339,7 +344,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
   gemm_kernel<EPI, BK><<<(unsigned)nblocks, GW * 64, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
-      gate_stride, cu, nseg, tiles_m, tiles_n);
+      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
   return ditk_check_launch("ditk_gemm");
 }
 

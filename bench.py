@@ -35,7 +35,7 @@ REFERENCE_STEPS_PER_S = 1000.0 / 3964.62
 # bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that counter's
 # reading for the CALIB_BYTES copy: FETCH 917467.5 KiB x 1.9997, WRITE 196581.8 KiB x 1.0000
 # (profiles/wan21_480p_cfg2_step_traffic.md).  Re-measure after kernel changes.
-ATTN_SELF_TRAFFIC_BYTES = (917548 * 1.9997 + 196597 * 1.0000) * 1024
+ATTN_SELF_TRAFFIC_BYTES = (917548 * 1.9997 + 196607 * 1.0000) * 1024
 
 
 # Other single-GPU workloads of the same step (reported per config; the default

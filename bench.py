@@ -144,7 +144,8 @@ def main():
         latent = step(latent)
     torch.cuda.synchronize()
 
-    prof = EventProfiler(enabled=True)
+    # only the roofline kernel's region is timed unless the breakdown is asked for
+    prof = EventProfiler(enabled=True, only=None if args.breakdown else {"attn_self"})
     model.profiler = prof
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -244,7 +245,7 @@ def run_sd35(args):
     for _ in range(args.warmup):
         latent = step(latent)
     torch.cuda.synchronize()
-    prof = EventProfiler(enabled=True)
+    prof = EventProfiler(enabled=True, only=None if args.breakdown else {"attn_joint"})
     model.profiler = prof
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()

@@ -40,6 +40,16 @@ def _check(t, name, dtype=None, dims=None):
         raise ValueError(f"{name} must be {dims}-D, got shape {tuple(t.shape)}")
 
 
+def to_device(data, dtype, device):
+    """Small host table -> device tensor without stalling the host: the values go
+    through pinned memory and a non-blocking copy on the current stream (a
+    pageable copy would wait for all work already queued on the stream)."""
+    host = torch.tensor(data, dtype=dtype)
+    if torch.device(device).type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
 def _rows(t, name):
     """2-D row-major view requirements: unit column stride, 16-byte aligned rows."""
     if t.dim() != 2 or t.stride(1) != 1:
@@ -59,7 +69,7 @@ class Segments:
         self.cu = [int(x) for x in cu]
         if not self.cu or self.cu[0] != 0 or any(b < a for a, b in zip(self.cu, self.cu[1:])):
             raise ValueError(f"cu_seqlens must start at 0 and be nondecreasing, got {self.cu}")
-        self.dev = torch.tensor(self.cu, dtype=torch.int32, device=device)
+        self.dev = to_device(self.cu, torch.int32, device)
         self._nseg, self._total = len(self.cu) - 1, self.cu[-1]
 
     @classmethod
@@ -154,8 +164,7 @@ class Rope:
 
     def __init__(self, cos_tab, sin_tab, grids, segments, t_pairs, h_pairs):
         self.cos, self.sin = cos_tab, sin_tab
-        self.grids = torch.tensor([list(map(int, g)) for g in grids], dtype=torch.int32,
-                                  device=cos_tab.device).reshape(-1)
+        self.grids = to_device([list(map(int, g)) for g in grids], torch.int32, cos_tab.device).reshape(-1)
         self.segments = segments
         self.t_pairs, self.h_pairs = int(t_pairs), int(h_pairs)
         if len(grids) != segments.nseg:

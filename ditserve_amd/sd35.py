@@ -310,7 +310,7 @@ class SD35Transformer:
             rows = h[seg_img.cu[m]:seg_img.cu[m + 1]]
             ops.linear(patches, self.pe_w, self.pe_b, "res", residual=self._pos(hp, wp), out=rows)
         c = ops.linear(torch.cat([t.to(device=dev, dtype=_BF16) for t in txts]), *self.ctx)
-        t = torch.tensor([float(x) for x in timesteps], dtype=torch.float32, device=dev)
+        t = ops.to_device([float(x) for x in timesteps], torch.float32, dev)
         te = ops.linear(ops.linear(ops.timestep_embedding(t, cfg.freq_dim), *self.te1, "silu"), *self.te2)
         pooled = torch.stack([p.reshape(-1) for p in pooleds]).to(device=dev, dtype=_BF16)
         temb = ops.linear(ops.linear(pooled, *self.pp1, "silu"), *self.pp2, "res", residual=te)

@@ -257,7 +257,7 @@ class WanTransformer:
         text_lens = [int(t.shape[-2]) for t in texts]
         seg_txt = Segments([0] + [sum(text_lens[: i + 1]) for i in range(len(text_lens))], dev)
         text = torch.cat([t.reshape(-1, cfg.text_dim).to(device=dev, dtype=_BF16) for t in texts])
-        t = torch.tensor([float(x) for x in timesteps], dtype=torch.float32, device=dev)
+        t = ops.to_device([float(x) for x in timesteps], torch.float32, dev)
         temb, projected, enc = self.condition(t, text)
         rope = ops.Rope(self.rope_cos, self.rope_sin, grids, seg, self.rope_pairs[0], self.rope_pairs[1])
         packet = dict(hidden=hidden, encoder=enc, temb=temb, projected=projected, rotary=rope,

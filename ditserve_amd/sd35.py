@@ -214,6 +214,25 @@ class SD35Transformer:
                 blk["nq2"], blk["nk2"] = per_head(f"{a2}.norm_q.weight"), per_head(f"{a2}.norm_k.weight")
                 blk["out2"] = (w(f"{a2}.to_out.0.weight"), f(f"{a2}.to_out.0.bias"))
             self.blocks.append(blk)
+        # Every AdaLN modulation projection (norm1, norm1_context of each block,
+        # norm_out) reads the same conditioning rows silu(temb), so all of them
+        # run as one GEMM per step over the weights stacked along N: one launch
+        # streams the ~1.5 GB of modulation weights instead of 49 launches with
+        # two rows each.  Per-layer entries become views into the stacked copy.
+        mods = [(blk, key) for blk in self.blocks for key in ("n1", "n1c")]
+        parts = [blk[key] for blk, key in mods] + [self.norm_out]
+        self.mod_w = torch.cat([p[0] for p in parts])
+        self.mod_b = torch.cat([p[1] for p in parts])
+        off = 0
+        for (blk, key), (pw, _) in zip(mods, parts):
+            n = pw.shape[0]
+            blk[key] = (self.mod_w[off:off + n], self.mod_b[off:off + n])
+            blk[key + "_cols"] = (off, off + n)
+            off += n
+        n = self.norm_out[0].shape[0]
+        self.norm_out = (self.mod_w[off:off + n], self.mod_b[off:off + n])
+        self.norm_out_cols = (off, off + n)
+        del parts
         self._pos_cache = {}
         self.profiler = _NULL_PROFILER
 
@@ -235,14 +254,14 @@ class SD35Transformer:
         ops.qk_norm_rope_(q, k, wq, wk, Dh, self.cfg.eps, per_head=True)
         return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh)
 
-    def _block(self, i, h, c, st, seg_img, seg_txt, seg_joint):
+    def _block(self, i, h, c, mod, seg_img, seg_txt, seg_joint):
         cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
         D, eps = cfg.dim, cfg.eps
         with prof.region("adaln"):
-            emb = ops.linear(st, *blk["n1"], "f32")  # [M, 6D or 9D]
+            emb = mod[:, slice(*blk["n1_cols"])]  # [M, 6D or 9D]
             nh = ops.adaln(h, emb[:, 0:D], emb[:, D:2 * D], seg_img, eps=eps)
             nh2 = ops.adaln(h, emb[:, 6 * D:7 * D], emb[:, 7 * D:8 * D], seg_img, eps=eps) if blk["dual"] else None
-            embc = ops.linear(st, *blk["n1c"], "f32")  # [M, 2D] (last) or [M, 6D]
+            embc = mod[:, slice(*blk["n1c_cols"])]  # [M, 2D] (last) or [M, 6D]
             if blk["last"]:  # AdaLN-Continuous: (scale, shift)
                 nc = ops.adaln(c, embc[:, D:2 * D], embc[:, 0:D], seg_txt, eps=eps)
             else:
@@ -250,13 +269,16 @@ class SD35Transformer:
         with prof.region("gemm_qkv"):
             qkv_i = ops.linear(nh, *blk["qkv"])
             qkv_t = ops.linear(nc, *blk["qkv_t"])
-        with prof.region("attn_joint"):
+        with prof.region("joint_prep"):
             D3 = 3 * D
             ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq"], blk["nk"], cfg.head_dim, eps, per_head=True)
             ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt"], blk["nkt"], cfg.head_dim, eps, per_head=True)
             joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
-            a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], joint[:, 2 * D:D3], seg_joint, seg_joint,
-                                      cfg.heads, cfg.head_dim)
+            vt = ops.transpose_v(joint[:, 2 * D:D3], cfg.heads, cfg.head_dim, seg_joint)
+        with prof.region("attn_joint"):
+            a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, seg_joint, seg_joint,
+                                      cfg.heads, cfg.head_dim, vt=vt)
+        with prof.region("joint_scatter"):
             a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
             a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
             ops.joint_scatter(a, a_img, a_txt, seg_img, seg_txt)
@@ -315,10 +337,11 @@ class SD35Transformer:
         pooled = torch.stack([p.reshape(-1) for p in pooleds]).to(device=dev, dtype=_BF16)
         temb = ops.linear(ops.linear(pooled, *self.pp1, "silu"), *self.pp2, "res", residual=te)
         st = ops.silu(temb)
+        mod = ops.linear(st, self.mod_w, self.mod_b, "f32")  # every block's modulation + norm_out
         for i in range(cfg.layers):
-            h, c = self._block(i, h, c, st, seg_img, seg_txt, seg_joint)
+            h, c = self._block(i, h, c, mod, seg_img, seg_txt, seg_joint)
         # epilogue: AdaLN-Continuous norm_out (scale, shift), proj_out, per-request unpatchify
-        embo = ops.linear(st, *self.norm_out, "f32")
+        embo = mod[:, slice(*self.norm_out_cols)]
         x = ops.adaln(h, embo[:, D:2 * D], embo[:, 0:D], seg_img, eps=cfg.eps)
         y = ops.linear(x, *self.proj_out)
         outs = []

@@ -401,12 +401,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   // Split interleave: the 16 score pairs of a tile are spread evenly over both
   // MFMA phases of the wave.  Per tile kt:
   //   phase 1: S(kt+1) = K(kt+1) Q^T   ||  P(kt) keys 32..63
-  //   (rescale check on keys 32..63)
+  //   (rescale check on all 64 keys of P(kt))
   //   phase 2: O += Vt(kt) P(kt)       ||  P(kt+1) keys 0..31
-  //   (rescale check on keys 0..31 of kt+1)
-  // The check of a half flags every half with a score above m + kLazy (its sum
-  // then exceeds 2^kLazy); the rescale raises m from the S registers still
-  // live, scales O and l, and recomputes the P values not yet folded into O.
+  // One check per tile, on the lane's row sum over both halves, before any of
+  // P(kt) reaches O: it flags every tile with a score above m + kLazy (that
+  // score alone makes the sum exceed 2^kLazy), and the rescale redoes the
+  // whole tile from K(kt), still resident in LDS.  Keys 0..31 of P(kt+1) are
+  // computed against the running m and checked with the rest of tile kt+1.
   auto pair_at = [&](const f32x16_t (&s)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int qb,
                      int kk, int r) {
     const int j = r >> 2, e = r & 3;
@@ -453,22 +454,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
         ops += item(k, n, pi) == 0 ? 4 : 3;
       }
     return ops;
-  };
-  auto half_max = [&](const f32x16_t& sk) {
-    float a = sk[0];
-#pragma unroll
-    for (int v = 1; v < 16; ++v) a = fmaxf(a, sk[v]);
-    return fmaxf(a, __shfl_xor(a, 32, 64)) * scale_log2;
-  };
-  auto raise_m = [&](int qb, float tile_max) {
-    const float m_new = fmaxf(m_run[qb], tile_max);
-    const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-    m_run[qb] = m_new;
-    l_run[qb] *= alpha;
-#pragma unroll
-    for (int d = 0; d < DT; ++d)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
   };
   auto steady_split = [&](int kt, f32x16_t (&s_cur)[QB][2], f32x16_t (&s_nxt)[QB][2],
                           uint32_t (&pf_cur)[QB][2][2][4], uint32_t (&pf_nxt)[QB][2][2][4],
@@ -519,7 +504,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       }
     }
     pin(pf_cur);
-    if (needs_rescale(rs1)) {
+    float rsum[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) rsum[qb] = rs0_cur[qb] + rs1[qb];
+    if (needs_rescale(rsum)) {
       // P(kt) keys 0..31 are not in O yet either: the whole tile is redone from
       // K(kt), still resident, so S(kt) keys 0..31 need not stay in registers
       rescale_tile(kt % KST, pf_cur, rs1, BN);
@@ -559,15 +547,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       }
     }
     pin(pf_nxt);
-    if (needs_rescale(rs0_nxt)) {
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        raise_m(qb, half_max(s_nxt[qb][0]));
-        rs0_nxt[qb] = 0.f;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) pair_at(s_nxt, pf_nxt, rs0_nxt, qb, 0, r);
-      }
-    }
     dma_wait();
     __syncthreads();
   };

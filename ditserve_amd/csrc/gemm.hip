@@ -33,32 +33,54 @@ enum Epilogue : int {
   EPI_SILU = 5,      // bf16(silu(bf16(acc + b)))
 };
 
-constexpr int GBM = 256;                     // tokens per workgroup tile
-constexpr int GBN = 256;                     // features per workgroup tile
-constexpr int GW = 8;                        // waves per workgroup: 2 x (GW/2) wave tiles
-constexpr int WTM = GBM / 2;                 // tokens per wave tile
-constexpr int WTN = GBN / (GW / 2);          // features per wave tile
-constexpr int LDS_STAGE_BYTES = 128 * 1024;  // k stages (reused by the epilogue staging)
+// Workgroup tile configurations.  A wave computes WTM tokens x 64 features (the
+// epilogue staging swizzle below assumes 64 features); the GW = WM x WN waves of
+// a workgroup are laid out WM along tokens and WN along features.
+//   TILE_LARGE  256 x 256, 8 waves of 128 x 64, 128 KiB of LDS stages, one
+//               workgroup per CU (two waves per SIMD).
+//   TILE_SMALL   64 x 128, 4 waves of 32 x 64, 72 KiB, two workgroups per CU:
+//               for GEMMs whose large tiles would leave CUs idle (the few hundred
+//               text rows of a step, two-row conditioning projections).
+// Both run the same MFMA (W rows as the A operand) over the same k-chunk order
+// with the same epilogue arithmetic, so an output element is bitwise the same
+// whichever tile computed it.
+enum TileCfg : int { TILE_LARGE = 0, TILE_SMALL = 1 };
+template <int T> struct Tile;
+template <> struct Tile<TILE_LARGE> {
+  static constexpr int GBM = 256, GBN = 256, WM = 2, WN = 4, LDS_BYTES = 128 * 1024, WAVES_PER_EU = 1;
+};
+template <> struct Tile<TILE_SMALL> {
+  static constexpr int GBM = 64, GBN = 128, WM = 2, WN = 2, LDS_BYTES = 72 * 1024, WAVES_PER_EU = 2;
+};
 
 // k-stage geometry for BK k values per stage (BK = 64 when K allows, else 32)
-template <int BK>
+template <int BK, int T>
 struct Stages {
+  static constexpr int GBM = Tile<T>::GBM;            // tokens per workgroup tile
+  static constexpr int GBN = Tile<T>::GBN;            // features per workgroup tile
+  static constexpr int GW = Tile<T>::WM * Tile<T>::WN;  // waves per workgroup
+  static constexpr int WTM = GBM / Tile<T>::WM;       // tokens per wave tile
+  static constexpr int WTN = GBN / Tile<T>::WN;       // features per wave tile
   static constexpr int GBK = BK;
   static constexpr int NCH = BK / 32;                 // 32-k MFMA chunks per stage
   static constexpr int CPRW = BK / 8;                 // 16-byte chunks per LDS row
   static constexpr int RPG = 64 / CPRW;               // rows filled by one DMA instruction (1 KiB)
-  static constexpr int NGRP = GBM / RPG;              // DMA instructions per operand and stage
-  static constexpr int NSTAGE = LDS_STAGE_BYTES / ((GBM + GBN) * BK * 2);
-  static constexpr int DPW = NGRP / GW;               // DMA instructions per operand, wave and stage
-  static_assert(GBM == GBN && (BK == 32 || BK == 64) && NSTAGE >= 2, "tile configuration");
+  static constexpr int DPW_A = GBM / RPG / GW;        // A DMA instructions per wave and stage
+  static constexpr int DPW_W = GBN / RPG / GW;        // W DMA instructions per wave and stage
+  static constexpr int ND = DPW_A + DPW_W;            // DMA instructions per wave and stage
+  static constexpr int NSTAGE = Tile<T>::LDS_BYTES / ((GBM + GBN) * BK * 2);
+  static_assert(WTN == 64 && DPW_A >= 1 && DPW_W >= DPW_A && DPW_A * GW * RPG == GBM &&
+                    DPW_W * GW * RPG == GBN && (BK == 32 || BK == 64) && NSTAGE >= 2 &&
+                    GW * WTM * WTN * 2 <= Tile<T>::LDS_BYTES,
+                "tile configuration");
   // LDS stage layout (A and W alike): row r of BK k-values = CPRW chunks of
   // 16 B, slot(r, u) = r*CPRW + (u ^ swz(r)).  A DMA instruction fills 64
   // contiguous slots (RPG whole rows); 16 consecutive lanes reading chunk u of
   // 16 consecutive rows hit 16 distinct 16-byte bank groups.
   static __device__ __forceinline__ int swz(int r) { return CPRW == 4 ? (r >> 2) & 3 : (r >> 1) & 7; }
-  // wait until at most `stages` DMA stages (2*DPW instructions each) of this wave are in flight
+  // wait until at most `stages` DMA stages (ND instructions each) of this wave are in flight
   static __device__ __forceinline__ void dma_wait(int stages) {
-    constexpr int P = 2 * DPW;
+    constexpr int P = ND;
     if (stages >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * P) : "memory");
     else if (stages == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(P) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -84,16 +106,17 @@ __device__ __forceinline__ void lds_dma16(const bf16_t* gsrc, u32x4_t* lds_slot0
 // features f = i*16 + 4*(lane/16) + e, token t = j*16 + lane % 16 of the wave
 // tile.  The bias is loaded after the k loop (holding it through the loop would
 // spill).
-template <int EPI, int BK>
-__global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
+template <int EPI, int BK, int T>
+__global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_EU) void gemm_kernel(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
-  using S = Stages<BK>;
-  constexpr int CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW = S::DPW;
-  constexpr int NCH = S::NCH;
-  constexpr int FI = WTN / 16, FJ = WTM / 16;  // feature / token fragments per wave (4, 8)
+  using S = Stages<BK, T>;
+  constexpr int GBM = S::GBM, GBN = S::GBN, GW = S::GW, WTM = S::WTM, WTN = S::WTN;
+  constexpr int CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW_A = S::DPW_A, DPW_W = S::DPW_W;
+  constexpr int ND = S::ND, NCH = S::NCH;
+  constexpr int FI = WTN / 16, FJ = WTM / 16;  // feature / token fragments per wave (4; 8 or 2)
   __shared__ u32x4_t lds[NSTAGE * (GBM + GBN) * CPRW];
   auto As = [&](int s) { return lds + s * (GBM * CPRW); };
   auto Ws = [&](int s) { return lds + NSTAGE * GBM * CPRW + s * (GBN * CPRW); };
@@ -111,28 +134,36 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ql = lane & 15, g = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const int wm = wave_u & 1, wn = wave_u >> 1;
+  const int wm = wave_u % Tile<T>::WM, wn = wave_u / Tile<T>::WM;
   const int a_row0 = wm * WTM, w_row0 = wn * WTN;
 
   const bf16_t* Ablk = A + (int64_t)m0 * lda;
   const bf16_t* Wblk = W + (int64_t)n0 * ldw;
-  uint32_t a_off[DPW], w_off[DPW];
+  uint32_t a_off[DPW_A], w_off[DPW_W];
 #pragma unroll
-  for (int i = 0; i < DPW; ++i) {
+  for (int i = 0; i < DPW_W; ++i) {
     const int gi = i * GW + wave_u;
     const int row = gi * RPG + lane / CPRW;
     const int ksw = ((lane % CPRW) ^ S::swz(row)) * 8;
-    a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + ksw);
+    if (i < DPW_A) a_off[i] = (uint32_t)(min(row, M - 1 - m0) * lda + ksw);
     w_off[i] = (uint32_t)(min(row, N - 1 - n0) * ldw + ksw);
   }
+  // DMA instruction d of a stage: A and W alternate while both have
+  // instructions left, then the remaining W ones
   auto dma_one = [&](int kt, int d) {
-    const int s = kt % NSTAGE, i = d >> 1, gi = i * GW + wave_u;
-    if ((d & 1) == 0) lds_dma16(Ablk + kt * BK + a_off[i], &As(s)[gi * 64]);
-    else lds_dma16(Wblk + kt * BK + w_off[i], &Ws(s)[gi * 64]);
+    const int s = kt % NSTAGE;
+    if (d < 2 * DPW_A) {
+      const int i = d >> 1, gi = i * GW + wave_u;
+      if ((d & 1) == 0) lds_dma16(Ablk + kt * BK + a_off[i], &As(s)[gi * 64]);
+      else lds_dma16(Wblk + kt * BK + w_off[i], &Ws(s)[gi * 64]);
+    } else {
+      const int i = d - DPW_A, gi = i * GW + wave_u;
+      lds_dma16(Wblk + kt * BK + w_off[i], &Ws(s)[gi * 64]);
+    }
   };
   auto issue = [&](int kt) {
 #pragma unroll
-    for (int d = 0; d < 2 * DPW; ++d) dma_one(kt, d);
+    for (int d = 0; d < ND; ++d) dma_one(kt, d);
   };
 
   // operand read base of chunk c: row x*16 + ql, 16-byte chunk c*4 + g (the
@@ -177,22 +208,31 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
   };
-  // group j of a chunk (operand set p for the feature fragments): the 4 MFMAs of
+  // group j of a chunk (operand set p for the feature fragments): the FI MFMAs of
   // token fragment j, then the reads of the next chunk (cn of stage sn): token
-  // fragment j into fx[j] and, every other group, a feature fragment into set p^1;
-  // and DMA issue j of stage kd
+  // fragment j into fx[j] and this group's share of the feature fragments into
+  // set p^1 (one every other group when FJ = 8, two per group when FJ = 2);
+  // and DMA instructions j, j + FJ, ... of stage kd
   auto step = [&](int j, int p, int sn, int cn, int kd, bool reads, bool dmas) {
 #pragma unroll
     for (int i = 0; i < FI; ++i)
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[p][i], fx[j], acc[i][j], 0, 0, 0);
     if (reads) {
       read_x(sn, cn, j);
-      if (j % 2 == 1) read_w(sn, cn, j / 2, fw[p ^ 1]);
+      if (FJ >= FI) {
+        if (j % (FJ / FI) == FJ / FI - 1) read_w(sn, cn, j / (FJ / FI), fw[p ^ 1]);
+      } else {
+#pragma unroll
+        for (int i = j * (FI / FJ); i < (j + 1) * (FI / FJ); ++i) read_w(sn, cn, i, fw[p ^ 1]);
+      }
     }
-    if (dmas && j < 2 * DPW) dma_one(kd, j);
+    if (dmas) {
+#pragma unroll
+      for (int d = j; d < ND; d += FJ) dma_one(kd, d);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
-  static_assert(FJ == 2 * FI && 2 * DPW <= FJ && (NCH % 2 == 0 || NCH == 1), "group layout");
+  static_assert((FJ % FI == 0 || FI % FJ == 0) && (NCH % 2 == 0 || NCH == 1), "group layout");
   // with one chunk per stage the next stage's feature fragments land in set 1:
   // swap the two sets after each stage (4 fragments, only the 32-k stage path)
   auto rotate = [&]() {
@@ -334,18 +374,39 @@ __global__ __launch_bounds__(GW * 64, 1) void gemm_kernel(
   }
 }
 
+template <int EPI, int BK, int T>
+int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
+                int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
+                int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream) {
+  using S = Stages<BK, T>;
+  const int tiles_m = (M + S::GBM - 1) / S::GBM, tiles_n = (N + S::GBN - 1) / S::GBN;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int64_t nblocks = (tiles + 7) / 8 * 8;
+  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
+  gemm_kernel<EPI, BK, T><<<(unsigned)nblocks, S::GW * 64, 0, stream>>>(
+      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
+      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
+  return ditk_check_launch("ditk_gemm");
+}
+
+// Small tiles when the large ones would number fewer than GEMM_SMALL_BELOW: the
+// choice cannot change a result, only how many CUs take part.  Measured per CU,
+// a small workgroup alone on a CU runs at about half a large one's rate and two
+// sharing one at about a quarter each, so small tiles (8 per large tile) win
+// while they fit about two per CU: 666-row text GEMMs 1.3-3x faster (54-72
+// large tiles), 8192 x 1536 1.25-1.5x slower (192 large tiles).
+#ifndef GEMM_SMALL_BELOW
+#define GEMM_SMALL_BELOW 128
+#endif
 template <int EPI, int BK>
 int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
            int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
            int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream) {
-  const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
-  const int64_t tiles = (int64_t)tiles_m * tiles_n;
-  const int64_t nblocks = (tiles + 7) / 8 * 8;
-  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
-  gemm_kernel<EPI, BK><<<(unsigned)nblocks, GW * 64, 0, stream>>>(
-      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
-      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
-  return ditk_check_launch("ditk_gemm");
+  using L = Tile<TILE_LARGE>;
+  const int64_t large_tiles = (int64_t)((M + L::GBM - 1) / L::GBM) * ((N + L::GBN - 1) / L::GBN);
+  if (large_tiles < GEMM_SMALL_BELOW)
+    return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }
 
 template <int EPI>

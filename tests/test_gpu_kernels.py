@@ -75,6 +75,29 @@ def test_gemm_rows_independent_of_packing():
     assert torch.equal(full[313:777], part)
 
 
+@pytest.mark.parametrize("epi", ["bias", "gelu", "f32", "gate_res"])
+@pytest.mark.parametrize("K", [1536, 96])
+def test_gemm_tile_configs_agree(epi, K):
+    """Large M runs 256x256 workgroup tiles, a few hundred rows the 64x128 ones;
+    both use the same MFMA, k order and epilogue arithmetic, so rows computed
+    in either are bitwise equal (K = 96 takes the 32-k stage path of both)."""
+    ops = _ops()
+    M, N = 8192, 2048  # 32 x 8 large tiles: the large configuration
+    a = randn((M, K), 40).to(DEV, torch.bfloat16)
+    w = randn((N, K), 41, 0.02).to(DEV, torch.bfloat16)
+    b = randn((N,), 42).to(DEV)
+    kw = {}
+    if epi == "gate_res":
+        kw = dict(residual=randn((M, N), 43).to(DEV, torch.bfloat16), gate=randn((2, N), 44).to(DEV),
+                  segments=_seg([0, 5000, M]))
+    full = ops.linear(a, w, b, epi, **kw)
+    lo, hi = 4700, 5333  # 633 rows across the segment boundary: 3 x 8 large tiles, so small ones run
+    if epi == "gate_res":
+        kw = dict(residual=kw["residual"][lo:hi].contiguous(), gate=kw["gate"], segments=_seg([0, 5000 - lo, hi - lo]))
+    part = ops.linear(a[lo:hi].contiguous(), w, b, epi, **kw)
+    assert torch.equal(full[lo:hi], part)
+
+
 def test_gemm_stage_depths_agree():
     """K % 64 == 0 runs 64-k LDS stages, otherwise 32-k stages; the MFMA k order is
     the same, so zero-padding K by 32 (forcing the 32-k path) changes no bit."""

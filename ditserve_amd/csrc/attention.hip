@@ -28,6 +28,13 @@
 // Query tiles start at each segment's first query and the key loop starts at
 // each segment's first key, so results are independent of packing: a request
 // packed with others is bitwise equal to the same request run alone.
+//
+// PRE (head_dim 64 only): Q arrives multiplied by softmax_scale*log2(e) — the
+// producer folds that factor into its QK-norm weight, so Q is still rounded to
+// bf16 once.  The S^T accumulators then start from a register block holding -m
+// instead of zero, and P = exp2(S) takes no fma: every live S register holds
+// q.k*scale*log2(e) - m_run, and whenever m_run moves by d the live S registers
+// and the block move by -d.
 #include "ditk_common.h"
 
 namespace {
@@ -126,7 +133,7 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 // Each K / Vt fragment read from LDS feeds QB MFMAs (one per 32-query block).
 // K(kt) sits in LDS stage kt % KST (kept resident for the rescale path while
 // later tiles stream in), Vt(kt) in stage kt % 2.
-template <int HD, int NW, int QB>
+template <int HD, int NW, int QB, bool PRE>
 __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
@@ -192,12 +199,16 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int v = 0; v < 16; ++v) o[qb][d][v] = 0.f;
+  static_assert(!PRE || (ATTN_SPLIT && HD == 64), "pre-scaled Q: split loop, head_dim 64");
+  constexpr float kOne = 1.0f;
+  const float sc = PRE ? kOne : scale_log2;  // S -> log2 units
   float m_run[QB], l_run[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_run[qb] = -INFINITY;
     l_run[qb] = 0.f;
   }
+  f32x16_t negm[QB];  // PRE: -m_run in every register, the S accumulators' start
 
   // ---- DMA (global -> LDS, 16 B per lane).  Instruction i of wave w fills
   // slots [g*64, g*64 + 64), g = i*NW + w: rows 8*(g%(rows/8)) .. +8 of chunk
@@ -286,7 +297,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     float a = fmaxf(sacc[0][0], sacc[1][0]);
 #pragma unroll
     for (int v = 1; v < 16; ++v) a = fmaxf(a, fmaxf(sacc[0][v], sacc[1][v]));
-    return fmaxf(a, __shfl_xor(a, 32, 64)) * scale_log2;
+    return fmaxf(a, __shfl_xor(a, 32, 64)) * sc;
   };
   // P = exp2(S*c - m) as bf16 B-operand fragments for one query block; returns
   // the fp32 row sum over keys < valid (key of register v in key tile kk:
@@ -300,8 +311,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e], scale_log2, neg_m));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e + 1], scale_log2, neg_m));
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e], sc, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kk][j * 8 + 2 * e + 1], sc, neg_m));
           pf[kk][j][e] = pack_bf2(p0, p1);
           const int key = kk * 32 + j * 16 + hh * 8 + 2 * e;
           rs += (key < valid ? p0 : 0.f) + (key + 1 < valid ? p1 : 0.f);
@@ -321,10 +332,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int qb = 0; qb < QB; ++qb) r |= !(rs[qb] <= kRescaleSum);
     return __any(r);
   };
-  auto rescale_from = [&](const f32x16_t (&sr)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
+  // sr holds S - bias[qb] in log2 units (bias 0: S computed from zero)
+  auto rescale_from = [&](const f32x16_t (&sr)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid,
+                          const float (&bias)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const float m_new = fmaxf(m_run[qb], row_max(sr[qb]));
+      const float m_new = fmaxf(m_run[qb], PRE ? row_max(sr[qb]) + bias[qb] : row_max(sr[qb]));
       const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
       m_run[qb] = m_new;
       l_run[qb] *= alpha;
@@ -332,13 +345,32 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       for (int d = 0; d < DT; ++d)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[qb][d][v] *= alpha;
-      rs[qb] = softmax_p(sr[qb], pf[qb], m_run[qb], valid);
+      rs[qb] = softmax_p(sr[qb], pf[qb], PRE ? m_run[qb] - bias[qb] : m_run[qb], valid);
     }
   };
   auto rescale_tile = [&](int kstage, uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int valid) {
     f32x16_t sr[QB][2];
     compute_s(kstage, sr);
-    rescale_from(sr, pf, rs, valid);
+    const float zero[QB] = {};
+    rescale_from(sr, pf, rs, valid, zero);
+  };
+  auto set_negm = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) negm[qb][v] = -m_run[qb];
+  };
+  // PRE: move the live S registers to a new reference m (after m_run rose from m_old)
+  auto rebias = [&](f32x16_t (&s)[QB][2], const float (&m_old)[QB]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float d = m_run[qb] - m_old[qb];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[qb][kk][v] -= d;
+    }
+    set_negm();
   };
   auto pv = [&](int s, const uint32_t (&pf)[QB][2][2][4]) {
 #pragma unroll
@@ -376,10 +408,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   auto last = [&](const f32x16_t (&s)[QB][2]) {
     const int valid = k_len - (nkt - 1) * BN;
     uint32_t pf[QB][2][2][4];
-    float rs[QB];
+    float rs[QB], bias[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s[qb], pf[qb], m_run[qb], valid);
-    if (needs_rescale(rs)) rescale_from(s, pf, rs, valid);
+    for (int qb = 0; qb < QB; ++qb) {
+      bias[qb] = PRE ? m_run[qb] : 0.f;
+      rs[qb] = softmax_p(s[qb], pf[qb], PRE ? 0.f : m_run[qb], valid);
+    }
+    if (needs_rescale(rs)) rescale_from(s, pf, rs, valid, bias);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
     pv((nkt - 1) & 1, pf);
@@ -394,6 +429,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     issue_v(0, 0);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) m_run[qb] = row_max(s_next[qb]);  // exact max of the first tile
+    if (PRE) {
+      const float zero[QB] = {};
+      rebias(s_next, zero);  // S(0) - m, and the -m block
+    }
     dma_wait();
     __syncthreads();
   }
@@ -411,8 +450,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   auto pair_at = [&](const f32x16_t (&s)[QB][2], uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], int qb,
                      int kk, int r) {
     const int j = r >> 2, e = r & 3;
-    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
-    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+    const float p0 = PRE ? __builtin_amdgcn_exp2f(s[qb][kk][j * 8 + 2 * e])
+                         : __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+    const float p1 = PRE ? __builtin_amdgcn_exp2f(s[qb][kk][j * 8 + 2 * e + 1])
+                         : __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
     pf[qb][kk][j][e] = pack_bf2(p0, p1);
     rs[qb] += p0 + p1;
   };
@@ -428,8 +469,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   };
   auto pair_a = [&](const f32x16_t (&s)[QB][2], float (&ph)[2], int qb, int kk, int r) {
     const int j = r >> 2, e = r & 3;
-    ph[0] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
-    ph[1] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+    if (PRE) {
+      ph[0] = __builtin_amdgcn_exp2f(s[qb][kk][j * 8 + 2 * e]);
+      ph[1] = __builtin_amdgcn_exp2f(s[qb][kk][j * 8 + 2 * e + 1]);
+    } else {
+      ph[0] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e], scale_log2, -m_run[qb]));
+      ph[1] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][j * 8 + 2 * e + 1], scale_log2, -m_run[qb]));
+    }
   };
   auto pair_b = [&](uint32_t (&pf)[QB][2][2][4], float (&rs)[QB], const float (&ph)[2], int qb, int kk, int r) {
     pf[qb][kk][r >> 2][r & 3] = pack_bf2(ph[0], ph[1]);
@@ -451,7 +497,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int k = 0; k < 2 * n; ++k)
       if ((k * slots) / (2 * n) == t) {
         int pi;
-        ops += item(k, n, pi) == 0 ? 4 : 3;
+        ops += item(k, n, pi) == 0 ? (PRE ? 2 : 4) : 3;
       }
     return ops;
   };
@@ -481,7 +527,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
             s_nxt[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                kf[cb][kk], qf[qb][c], c == 0 ? f32x16_t{} : s_nxt[qb][kk], 0, 0, 0);
+                kf[cb][kk], qf[qb][c], c == 0 ? (PRE ? negm[qb] : f32x16_t{}) : s_nxt[qb][kk], 0, 0, 0);
           slot_items(slot, SLOTS, 8 * QB, s_cur, pf_cur, rs1, ph1, 1);
         }
         if (c + 1 < NC) {
@@ -510,7 +556,11 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     if (needs_rescale(rsum)) {
       // P(kt) keys 0..31 are not in O yet either: the whole tile is redone from
       // K(kt), still resident, so S(kt) keys 0..31 need not stay in registers
+      float m_old[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) m_old[qb] = m_run[qb];
       rescale_tile(kt % KST, pf_cur, rs1, BN);
+      if (PRE) rebias(s_nxt, m_old);  // S(kt+1) was started from the old -m
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) rs0_cur[qb] = 0.f;
     }
@@ -689,11 +739,12 @@ DITK_EXPORT int ditk_transpose_v(const void* v, int64_t ldv, void* vt, int64_t v
   return ditk_check_launch("ditk_transpose_v");
 }
 
-DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k, int64_t ldk,
-                                       const void* vt, int64_t vt_ld, void* o, int64_t ldo,
-                                       float* lse, int64_t lse_ld, const int32_t* cu_q,
-                                       const int32_t* cu_k, int nseg, int Tq, int heads,
-                                       int head_dim, float softmax_scale, hipStream_t stream) {
+namespace {
+// shared checks and launch of both attention entry points; sl2 = the factor that
+// takes q.k to log2 units inside the kernel (unused when pre)
+int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* vt, int64_t vt_ld, void* o,
+                 int64_t ldo, float* lse, int64_t lse_ld, const int32_t* cu_q, const int32_t* cu_k, int nseg, int Tq,
+                 int heads, int head_dim, float sl2, bool pre, hipStream_t stream) {
   DITK_REQUIRE(q && k && vt && o && cu_q && cu_k, "ditk_flash_attn_varlen: null tensor");
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_flash_attn_varlen: head_dim must be 64 or 128, got %d", head_dim);
   DITK_REQUIRE(nseg > 0 && heads > 0 && Tq >= 0, "ditk_flash_attn_varlen: bad sizes");
@@ -701,11 +752,9 @@ DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k
                "ditk_flash_attn_varlen: leading dims must be multiples of 8 (ldo of 4)");
   DITK_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)vt % 16) == 0 &&
                ((uintptr_t)o % 8) == 0, "ditk_flash_attn_varlen: misaligned tensor");
-  DITK_REQUIRE(softmax_scale > 0.f, "ditk_flash_attn_varlen: softmax_scale must be > 0");
   // the kernel addresses a 64-row K tile and an HD-row Vt tile with 32-bit element offsets
   DITK_REQUIRE(ldk < (1ll << 24) && vt_ld < (1ll << 24), "ditk_flash_attn_varlen: ldk / vt_ld too large");
   if (Tq == 0) return 0;
-  const float sl2 = softmax_scale * 1.4426950408889634f;
   const int64_t hs = (int64_t)head_dim * vt_ld;
   auto run = [&](auto kernel, int bm, int threads) -> int {
     const int tiles_bound = (Tq + bm - 1) / bm + nseg;
@@ -718,10 +767,33 @@ DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k
     return 0;
   };
   int rc;
-  if (head_dim == 128)
-    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+  if (pre)
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+  else if (head_dim == 128)
+    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   else
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
+}
+}  // namespace
+
+DITK_EXPORT int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                       const void* vt, int64_t vt_ld, void* o, int64_t ldo,
+                                       float* lse, int64_t lse_ld, const int32_t* cu_q,
+                                       const int32_t* cu_k, int nseg, int Tq, int heads,
+                                       int head_dim, float softmax_scale, hipStream_t stream) {
+  DITK_REQUIRE(softmax_scale > 0.f, "ditk_flash_attn_varlen: softmax_scale must be > 0");
+  return flash_launch(q, ldq, k, ldk, vt, vt_ld, o, ldo, lse, lse_ld, cu_q, cu_k, nseg, Tq, heads, head_dim,
+                      softmax_scale * 1.4426950408889634f, false, stream);
+}
+
+DITK_EXPORT int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                                   const void* vt, int64_t vt_ld, void* o, int64_t ldo,
+                                                   float* lse, int64_t lse_ld, const int32_t* cu_q,
+                                                   const int32_t* cu_k, int nseg, int Tq, int heads,
+                                                   int head_dim, hipStream_t stream) {
+  DITK_REQUIRE(head_dim == 64, "ditk_flash_attn_varlen_q_prescaled: head_dim must be 64, got %d", head_dim);
+  return flash_launch(q, ldq, k, ldk, vt, vt_ld, o, ldo, lse, lse_ld, cu_q, cu_k, nseg, Tq, heads, head_dim,
+                      1.0f, true, stream);
 }

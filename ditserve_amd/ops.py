@@ -279,13 +279,18 @@ def transpose_v(v, heads, head_dim, segments, out=None):
     return out
 
 
+LOG2E = 1.4426950408889634
+
+
 def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None, return_lse=False,
-                      out=None, vt=None):
+                      out=None, vt=None, q_prescaled=False):
     """Block-diagonal varlen attention on packed row views.
 
     q [Tq, heads*head_dim], k/v [Tk, heads*head_dim] bf16 (row strides may
     differ, e.g. slices of a fused QKV buffer).  Returns out [Tq, heads*head_dim]
-    (and lse [heads, Tq] fp32, natural log, when return_lse)."""
+    (and lse [heads, Tq] fp32, natural log, when return_lse).  q_prescaled
+    (head_dim 64): q already holds q * softmax_scale * log2(e), as a QK-norm
+    whose weight carries that factor produces it; softmax_scale must be None."""
     _check(q, "q", _BF16, 2)
     _check(k, "k", _BF16, 2)
     width = heads * head_dim
@@ -310,6 +315,13 @@ def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None
         out = torch.empty((Tq, width), dtype=_BF16, device=q.device)
     ldo = _rows(out, "out")
     lse = torch.empty((heads, Tq), dtype=torch.float32, device=q.device) if return_lse else None
+    if q_prescaled:
+        if softmax_scale is not None:
+            raise ValueError("q_prescaled carries the softmax scale in q: pass softmax_scale=None")
+        _lib.call("ditk_flash_attn_varlen_q_prescaled", _ptr(q), ldq, _ptr(k), ldk, _ptr(vt), vt.shape[2],
+                  _ptr(out), ldo, _ptr(lse), Tq, _ptr(seg_q.dev), _ptr(seg_k.dev), seg_q.nseg, Tq, heads,
+                  head_dim, _stream())
+        return (out, lse) if return_lse else out
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
     _lib.call("ditk_flash_attn_varlen", _ptr(q), ldq, _ptr(k), ldk, _ptr(vt), vt.shape[2], _ptr(out), ldo,
               _ptr(lse), Tq, _ptr(seg_q.dev), _ptr(seg_k.dev), seg_q.nseg, Tq, heads, head_dim, scale, _stream())

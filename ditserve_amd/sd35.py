@@ -19,6 +19,7 @@ Block (sd35_batch.py:647-708), per JointTransformerBlock:
   blocks); gated residuals; GELU-tanh FFNs on image and text.
 """
 import dataclasses
+import math
 
 import torch
 
@@ -183,6 +184,8 @@ class SD35Transformer:
         self.ctx = (w("context_embedder.weight"), f("context_embedder.bias"))
         self.norm_out = (w("norm_out.linear.weight"), f("norm_out.linear.bias"))
         self.proj_out = (w("proj_out.weight"), f("proj_out.bias"))
+        self._q_pre = cfg.head_dim == 64
+        self._q_mult = ops.LOG2E / math.sqrt(cfg.head_dim)
         self.blocks = []
         for i in range(cfg.layers):
             b = f"transformer_blocks.{i}"
@@ -213,6 +216,13 @@ class SD35Transformer:
                                torch.cat([f(f"{a2}.to_q.bias"), f(f"{a2}.to_k.bias"), f(f"{a2}.to_v.bias")]))
                 blk["nq2"], blk["nk2"] = per_head(f"{a2}.norm_q.weight"), per_head(f"{a2}.norm_k.weight")
                 blk["out2"] = (w(f"{a2}.to_out.0.weight"), f(f"{a2}.to_out.0.bias"))
+            # head_dim 64: the q-side RMSNorm weights carry softmax_scale * log2(e),
+            # so the normed q leaves the norm kernel pre-scaled (still one bf16
+            # rounding) and attention skips its per-score scaling
+            if self._q_pre:
+                for key in ("nq", "nqt", "nq2"):
+                    if key in blk:
+                        blk[key + "_pre"] = blk[key] * self._q_mult
             self.blocks.append(blk)
         # Every AdaLN modulation projection (norm1, norm1_context of each block,
         # norm_out) reads the same conditioning rows silu(temb), so all of them
@@ -248,11 +258,12 @@ class SD35Transformer:
 
     # ------------------------------------------------------------------ pieces
     def _attention(self, qkv, seg, wq, wk):
-        """Per-head QK RMSNorm (in place on the qkv buffer) + varlen flash over seg."""
+        """Per-head QK RMSNorm (in place on the qkv buffer) + varlen flash over seg
+        (wq already carries the pre-scale when self._q_pre)."""
         D, H, Dh = self.cfg.dim, self.cfg.heads, self.cfg.head_dim
         q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
         ops.qk_norm_rope_(q, k, wq, wk, Dh, self.cfg.eps, per_head=True)
-        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh)
+        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh, q_prescaled=self._q_pre)
 
     def _block(self, i, h, c, mod, seg_img, seg_txt, seg_joint):
         cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
@@ -271,13 +282,16 @@ class SD35Transformer:
             qkv_t = ops.linear(nc, *blk["qkv_t"])
         with prof.region("joint_prep"):
             D3 = 3 * D
-            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq"], blk["nk"], cfg.head_dim, eps, per_head=True)
-            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt"], blk["nkt"], cfg.head_dim, eps, per_head=True)
+            pre = "_pre" if self._q_pre else ""
+            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq" + pre], blk["nk"], cfg.head_dim, eps,
+                              per_head=True)
+            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt" + pre], blk["nkt"], cfg.head_dim, eps,
+                              per_head=True)
             joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
             vt = ops.transpose_v(joint[:, 2 * D:D3], cfg.heads, cfg.head_dim, seg_joint)
         with prof.region("attn_joint"):
             a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, seg_joint, seg_joint,
-                                      cfg.heads, cfg.head_dim, vt=vt)
+                                      cfg.heads, cfg.head_dim, vt=vt, q_prescaled=self._q_pre)
         with prof.region("joint_scatter"):
             a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
             a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
@@ -287,7 +301,7 @@ class SD35Transformer:
         if blk["dual"]:
             with prof.region("attn_dual"):
                 qkv2 = ops.linear(nh2, *blk["qkv2"])
-                a2 = self._attention(qkv2, seg_img, blk["nq2"], blk["nk2"])
+                a2 = self._attention(qkv2, seg_img, blk["nq2_pre" if self._q_pre else "nq2"], blk["nk2"])
                 ops.linear(a2, *blk["out2"], "gate_res", residual=h, gate=emb[:, 8 * D:9 * D], segments=seg_img, out=h)
         with prof.region("ffn"):
             n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)

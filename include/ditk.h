@@ -105,6 +105,20 @@ int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k, int64_t ld
                            ditk_stream_t stream);
 
 /*
+ * ditk_flash_attn_varlen with q already multiplied by softmax_scale * log2(e)
+ * (head_dim 64 only).  A producer that folds that factor into its QK-norm weight
+ * still rounds q to bf16 once, and the kernel then starts its score accumulators
+ * at -max and exponentiates them directly, one fused multiply-add per score fewer.
+ * No reference counterpart: used by the SD3.5 joint and dual attention, which
+ * replace the reference's SD3.5 varlen slot (sd35_batch.py:19-119,448-486) with
+ * their per-head RMSNorm weight pre-multiplied.
+ */
+int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* vt,
+                                       int64_t vt_ld, void* o, int64_t ldo, float* lse, int64_t lse_ld,
+                                       const int32_t* cu_q, const int32_t* cu_k, int nseg, int Tq, int heads,
+                                       int head_dim, ditk_stream_t stream);
+
+/*
  * latent [C, F, H, W] bf16 -> patches [S, C*pt*ph*pw] bf16 (Conv3d weight order).
  * Replaces: the patch_embedding input gather — transformer_wan.py:328-329.
  */

@@ -241,6 +241,53 @@ def test_attention_rising_scores(Dh):
     assert_close(out, _attn_ref(q, k, v, cu, cu, H, Dh), cos_min=0.9999, rel_max=1e-2, label=f"rising Dh={Dh}")
 
 
+@pytest.mark.parametrize("case", ["random", "rising"])
+@pytest.mark.parametrize("lens", [[1], [64, 65], [300, 1, 129, 511], [1025]])
+def test_attention_q_prescaled(case, lens):
+    """head_dim 64 with q already multiplied by softmax_scale*log2(e): the kernel starts its
+    score accumulators at -max and must move them whenever the max rises (rising scores
+    force that in every tile).  Reference: the oracle on the same bf16 q' rescaled back by
+    ln 2 * sqrt(Dh) in fp32, so that its softmax(q.k / sqrt(Dh)) equals 2^(q'.k)."""
+    ops = _ops()
+    H, Dh = 3, 64
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    T = cu[-1]
+    if case == "random":
+        q, k, v = _attn_case(cu, cu, H, Dh, 90, scale_in=2.0)
+    else:
+        g = torch.Generator().manual_seed(91)
+        u = torch.randn(H, Dh, generator=g)
+        u = u / u.norm(dim=1, keepdim=True)
+        sign = torch.where(torch.arange(T) % 2 == 0, 1.0, -1.0)
+        q = (math.sqrt(Dh) * sign[:, None, None] * u[None]).expand(T, H, Dh)
+        pos = torch.cat([torch.arange(cu[m + 1] - cu[m], dtype=torch.float32) for m in range(len(cu) - 1)])
+        k = 0.3 * pos[:, None, None] * u[None] + 0.1 * torch.randn(T, H, Dh, generator=g)
+        v = torch.randn(T, H, Dh, generator=g)
+        q, k, v = (bf(t.reshape(T, H * Dh)) for t in (q, k, v))
+    qp = bf(q * (ops.LOG2E / math.sqrt(Dh)))  # what a QK-norm with the folded weight emits
+    seg = _seg(cu)
+    out, lse = ops.flash_attn_varlen(qp.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16),
+                                     v.to(DEV, torch.bfloat16), seg, seg, H, Dh, return_lse=True, q_prescaled=True)
+    q_ref = qp * (math.log(2.0) * math.sqrt(Dh))
+    ref = _attn_ref(q_ref, k, v, cu, cu, H, Dh)
+    assert_close(out.float().cpu(), ref, cos_min=0.9999, rel_max=1e-2, label=f"prescaled {case} {lens}")
+    for m in range(len(lens)):
+        s0, s1 = cu[m], cu[m + 1]
+        qh, kh = q_ref[s0:s1].view(-1, H, Dh).transpose(0, 1), k[s0:s1].view(-1, H, Dh).transpose(0, 1)
+        ref_lse = torch.logsumexp((qh @ kh.transpose(1, 2)) / math.sqrt(Dh), dim=-1)
+        assert torch.allclose(lse[:, s0:s1].cpu(), ref_lse, atol=2e-3, rtol=1e-4)
+
+
+def test_attention_q_prescaled_rejects_head_dim_128():
+    ops = _ops()
+    x = torch.zeros((64, 128), dtype=torch.bfloat16, device=DEV)
+    seg = _seg([0, 64])
+    with pytest.raises(RuntimeError, match="head_dim must be 64"):
+        ops.flash_attn_varlen(x, x, x, seg, seg, 1, 128, q_prescaled=True)
+
+
 @pytest.mark.parametrize("Dh", [128, 64])
 def test_cross_attention_text_blocks(Dh):
     ops = _ops()

@@ -370,7 +370,12 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
       }
       v = pack8(x);
     }
-    *reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n) = v;
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n);
+    // large-tile outputs (>= 16 MB) are streamed: the next kernel reads them back
+    // from HBM anyway, and non-temporal stores measured 2.6-3.6% faster on the
+    // K = 1536 block GEMMs (qkv, ffn up, o-proj), unchanged on ffn down
+    if (T == TILE_LARGE) __builtin_nontemporal_store(v, dst);
+    else *dst = v;
   }
 }
 

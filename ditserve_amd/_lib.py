@@ -32,6 +32,9 @@ SIGNATURES = {
                                        _P, c_int, c_int, c_int, c_int, c_float, _P]),
     "ditk_flash_attn_varlen_q_prescaled": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64,
                                                    _P, _P, c_int, c_int, c_int, c_int, _P]),
+    "ditk_joint_attn_q_prescaled": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, _P, c_int64,
+                                            _P, _P, _P, c_int, c_int, c_int, c_int, _P]),
+    "ditk_transpose_v_joint": (c_int, [_P, _P, c_int64, _P, c_int64, c_int, c_int, c_int, _P, _P, _P, c_int, _P]),
     "ditk_patchify": (c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
     "ditk_unpatchify": (c_int, [_P, c_int64, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
     "ditk_timestep_embedding": (c_int, [_P, _P, c_int, c_int, c_float, _P]),

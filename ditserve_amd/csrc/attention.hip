@@ -35,6 +35,13 @@
 // instead of zero, and P = exp2(S) takes no fma: every live S register holds
 // q.k*scale*log2(e) - m_run, and whenever m_run moves by d the live S registers
 // and the block move by -d.
+//
+// JOINT (with PRE): each joint segment's rows come from two packed sources with
+// the same leading dimension — row j of segment m is row cu_a[m] + j of the
+// "a" operand (image tokens) while j < len_a(m), else row cu_b[m] + j - len_a(m)
+// of the "b" operand (text tokens) — for Q, K and O alike, so SD3.5's image and
+// text projections feed joint attention, and take its output, without a gather
+// or scatter copy.  Results are bitwise those of the gathered layout.
 #include "ditk_common.h"
 
 namespace {
@@ -133,12 +140,14 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 // Each K / Vt fragment read from LDS feeds QB MFMAs (one per 32-query block).
 // K(kt) sits in LDS stage kt % KST (kept resident for the rescale path while
 // later tiles stream in), Vt(kt) in stage kt % 2.
-template <int HD, int NW, int QB, bool PRE>
+template <int HD, int NW, int QB, bool PRE, bool JOINT>
 __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
     float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
-    const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
+    const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2,
+    const bf16_t* __restrict__ Qb, const bf16_t* __restrict__ Kb, bf16_t* __restrict__ Ob,
+    const int32_t* __restrict__ cu_a, const int32_t* __restrict__ cu_b) {
   constexpr int BM = NW * QB * 32;       // queries per workgroup
   constexpr int NC = HD / 16;            // 16-wide k chunks of the head dim
   constexpr int KCH = HD / 8;            // 16-byte chunks per K row
@@ -173,6 +182,15 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   const bf16_t* Qh = Q + (int64_t)head * HD;
   const bf16_t* Kh = Kp + (int64_t)head * HD + (int64_t)k_beg * ldk;
   const bf16_t* Vh = Vt + (int64_t)head * vt_hs + pk;
+  // JOINT: row j of this segment -> its row in the a or b operand
+  int a0 = 0, len_a = 0, b0 = 0;
+  if (JOINT) {
+    a0 = cu_a[seg];
+    len_a = cu_a[seg + 1] - a0;
+    b0 = cu_b[seg];
+  }
+  auto src_row = [&](int j) -> int64_t { return j < len_a ? (int64_t)(a0 + j) : (int64_t)(b0 + j - len_a); };
+  static_assert(!JOINT || PRE, "joint sources: pre-scaled kernel only");
 
   // ---- Q fragments (B operand of S^T): lane -> query l32 of block qb, k-slot hh*8..+8
   bf16x8_t qf[QB][NC];
@@ -182,7 +200,15 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int c = 0; c < NC; ++c) {
       u32x4_t v = u32x4_t{0, 0, 0, 0};
       const int qrow = qrow0 + 32 * qb;
-      if (qrow < q_end) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
+      if (qrow < q_end) {
+        if (JOINT) {
+          const int j = qrow - cu_q[seg];
+          const bf16_t* src = (j < len_a ? Qh : Qb + (int64_t)head * HD) + src_row(j) * ldq;
+          v = *reinterpret_cast<const u32x4_t*>(src + c * 16 + hh * 8);
+        } else {
+          v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * ldq + c * 16 + hh * 8);
+        }
+      }
       qf[qb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
   // consume the Q loads here, so the compiler's own vmcnt wait for them sits
@@ -237,6 +263,16 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   }
   auto issue_k = [&](int kt, int s) {
     const int kb = kt * BN;
+    if (JOINT) {
+      const bf16_t* ka = Kp + (int64_t)head * HD;
+      const bf16_t* kbp = Kb + (int64_t)head * HD;
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int j = min(kb + k_row[i], k_len - 1);
+        lds_dma16((j < len_a ? ka : kbp) + src_row(j) * ldk + k_col[i], &Ks[s][(i * NW + wave_u) * 64]);
+      }
+      return;
+    }
     const bf16_t* base = Kh + (int64_t)kb * ldk;
     if (kb + BN <= k_len) {
 #pragma unroll
@@ -657,6 +693,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     if (qrow < q_end) {
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       bf16_t* orow = O + (int64_t)qrow * ldo + (int64_t)head * HD;
+      if (JOINT) {
+        const int j = qrow - cu_q[seg];
+        orow = (j < len_a ? O : Ob) + src_row(j) * ldo + (int64_t)head * HD;
+      }
 #pragma unroll
       for (int d = 0; d < DT; ++d)
 #pragma unroll
@@ -674,11 +714,15 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
 
 // V [Tk, ldv] (head h at columns h*HD..) -> Vt [heads][HD][vt_ld], per-segment
 // 64-aligned columns, zero padding.  One workgroup per (64-key tile, head).
+// With cu_a != nullptr the segment's rows come from V (rows cu_a[m] + j) and Vb
+// (rows cu_b[m] + j - len_a(m)), as in the joint attention kernel.
 template <int HD>
 __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restrict__ V, int64_t ldv,
                                                           bf16_t* __restrict__ Vt, int64_t vt_ld,
                                                           int64_t vt_hs, const int32_t* __restrict__ cu,
-                                                          int nseg) {
+                                                          int nseg, const bf16_t* __restrict__ Vb,
+                                                          const int32_t* __restrict__ cu_a,
+                                                          const int32_t* __restrict__ cu_b) {
   constexpr int PITCH = HD + 2;  // u16 pitch: odd word stride spreads column reads over banks
   __shared__ bf16_t tile[BN * PITCH];
   int t = blockIdx.x;
@@ -693,7 +737,16 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
   for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
     int r = idx / CH, ch = idx % CH;
     u32x4_t v = u32x4_t{0, 0, 0, 0};
-    if (k0 + r < k_end) v = *reinterpret_cast<const u32x4_t*>(Vh + (int64_t)(k0 + r) * ldv + ch * 8);
+    if (k0 + r < k_end) {
+      if (cu_a != nullptr) {
+        const int j = t * BN + r, len_a = cu_a[seg + 1] - cu_a[seg];
+        const bf16_t* src = j < len_a ? Vh + (int64_t)(cu_a[seg] + j) * ldv
+                                      : Vb + (int64_t)head * HD + (int64_t)(cu_b[seg] + j - len_a) * ldv;
+        v = *reinterpret_cast<const u32x4_t*>(src + ch * 8);
+      } else {
+        v = *reinterpret_cast<const u32x4_t*>(Vh + (int64_t)(k0 + r) * ldv + ch * 8);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       tile[r * PITCH + ch * 8 + 2 * i] = (bf16_t)(v[i] & 0xffffu);
@@ -719,24 +772,42 @@ DITK_EXPORT int64_t ditk_vt_columns(int64_t Tk, int nseg) {
   return ((Tk + BN - 1) / BN + (int64_t)nseg) * BN;
 }
 
-DITK_EXPORT int ditk_transpose_v(const void* v, int64_t ldv, void* vt, int64_t vt_ld, int Tk,
-                                 int heads, int head_dim, const int32_t* cu_k, int nseg,
-                                 hipStream_t stream) {
+namespace {
+int transpose_launch(const void* v, const void* vb, int64_t ldv, void* vt, int64_t vt_ld, int Tk, int heads,
+                     int head_dim, const int32_t* cu_k, const int32_t* cu_a, const int32_t* cu_b, int nseg,
+                     hipStream_t stream) {
   DITK_REQUIRE(v && vt && cu_k, "ditk_transpose_v: null tensor");
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_transpose_v: head_dim must be 64 or 128");
   DITK_REQUIRE(nseg > 0 && heads > 0 && Tk >= 0, "ditk_transpose_v: bad sizes");
   DITK_REQUIRE(ldv % 8 == 0 && vt_ld % 8 == 0, "ditk_transpose_v: leading dims must be multiples of 8");
   DITK_REQUIRE(vt_ld >= ditk_vt_columns(Tk, nseg), "ditk_transpose_v: vt_ld=%lld < required %lld",
                (long long)vt_ld, (long long)ditk_vt_columns(Tk, nseg));
-  DITK_REQUIRE(((uintptr_t)v % 16) == 0 && ((uintptr_t)vt % 16) == 0, "ditk_transpose_v: misaligned");
+  DITK_REQUIRE(((uintptr_t)v % 16) == 0 && ((uintptr_t)vt % 16) == 0 && ((uintptr_t)vb % 16) == 0,
+               "ditk_transpose_v: misaligned");
   if (Tk == 0) return 0;
   dim3 grid((unsigned)((Tk + BN - 1) / BN + nseg), (unsigned)heads);
   const int64_t hs = (int64_t)head_dim * vt_ld;
   if (head_dim == 128)
-    transpose_v_kernel<128><<<grid, 256, 0, stream>>>((const bf16_t*)v, ldv, (bf16_t*)vt, vt_ld, hs, cu_k, nseg);
+    transpose_v_kernel<128><<<grid, 256, 0, stream>>>((const bf16_t*)v, ldv, (bf16_t*)vt, vt_ld, hs, cu_k, nseg,
+                                                       (const bf16_t*)vb, cu_a, cu_b);
   else
-    transpose_v_kernel<64><<<grid, 256, 0, stream>>>((const bf16_t*)v, ldv, (bf16_t*)vt, vt_ld, hs, cu_k, nseg);
+    transpose_v_kernel<64><<<grid, 256, 0, stream>>>((const bf16_t*)v, ldv, (bf16_t*)vt, vt_ld, hs, cu_k, nseg,
+                                                      (const bf16_t*)vb, cu_a, cu_b);
   return ditk_check_launch("ditk_transpose_v");
+}
+}  // namespace
+
+DITK_EXPORT int ditk_transpose_v(const void* v, int64_t ldv, void* vt, int64_t vt_ld, int Tk,
+                                 int heads, int head_dim, const int32_t* cu_k, int nseg,
+                                 hipStream_t stream) {
+  return transpose_launch(v, nullptr, ldv, vt, vt_ld, Tk, heads, head_dim, cu_k, nullptr, nullptr, nseg, stream);
+}
+
+DITK_EXPORT int ditk_transpose_v_joint(const void* v_a, const void* v_b, int64_t ldv, void* vt, int64_t vt_ld,
+                                       int T_joint, int heads, int head_dim, const int32_t* cu_a,
+                                       const int32_t* cu_b, const int32_t* cu_joint, int nseg, hipStream_t stream) {
+  DITK_REQUIRE(v_a && v_b && cu_a && cu_b, "ditk_transpose_v_joint: null tensor");
+  return transpose_launch(v_a, v_b, ldv, vt, vt_ld, T_joint, heads, head_dim, cu_joint, cu_a, cu_b, nseg, stream);
 }
 
 namespace {
@@ -744,7 +815,13 @@ namespace {
 // takes q.k to log2 units inside the kernel (unused when pre)
 int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* vt, int64_t vt_ld, void* o,
                  int64_t ldo, float* lse, int64_t lse_ld, const int32_t* cu_q, const int32_t* cu_k, int nseg, int Tq,
-                 int heads, int head_dim, float sl2, bool pre, hipStream_t stream) {
+                 int heads, int head_dim, float sl2, bool pre, hipStream_t stream, const void* qb = nullptr,
+                 const void* kb = nullptr, void* ob = nullptr, const int32_t* cu_a = nullptr,
+                 const int32_t* cu_b = nullptr) {
+  const bool joint = cu_a != nullptr;
+  DITK_REQUIRE(!joint || (pre && qb && kb && ob && cu_b), "ditk_joint_attn: needs both sources and both tables");
+  DITK_REQUIRE(!joint || (((uintptr_t)qb % 16) == 0 && ((uintptr_t)kb % 16) == 0 && ((uintptr_t)ob % 8) == 0),
+               "ditk_joint_attn: misaligned tensor");
   DITK_REQUIRE(q && k && vt && o && cu_q && cu_k, "ditk_flash_attn_varlen: null tensor");
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_flash_attn_varlen: head_dim must be 64 or 128, got %d", head_dim);
   DITK_REQUIRE(nseg > 0 && heads > 0 && Tq >= 0, "ditk_flash_attn_varlen: bad sizes");
@@ -763,16 +840,19 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
     kernel<<<(unsigned)nblocks, threads, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk,
                                                       (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld,
-                                                      cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+                                                      cu_q, cu_k, nseg, heads, tiles_bound, sl2, (const bf16_t*)qb,
+                                                      (const bf16_t*)kb, (bf16_t*)ob, cu_a, cu_b);
     return 0;
   };
   int rc;
-  if (pre)
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+  if (joint)
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true, true>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+  else if (pre)
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   else if (head_dim == 128)
-    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB, false, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   else
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, false, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
   if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
 }
@@ -796,4 +876,15 @@ DITK_EXPORT int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, c
   DITK_REQUIRE(head_dim == 64, "ditk_flash_attn_varlen_q_prescaled: head_dim must be 64, got %d", head_dim);
   return flash_launch(q, ldq, k, ldk, vt, vt_ld, o, ldo, lse, lse_ld, cu_q, cu_k, nseg, Tq, heads, head_dim,
                       1.0f, true, stream);
+}
+
+DITK_EXPORT int ditk_joint_attn_q_prescaled(const void* q_a, const void* q_b, int64_t ldq, const void* k_a,
+                                            const void* k_b, int64_t ldk, const void* vt, int64_t vt_ld, void* o_a,
+                                            void* o_b, int64_t ldo, const int32_t* cu_a, const int32_t* cu_b,
+                                            const int32_t* cu_joint, int nseg, int T_joint, int heads,
+                                            int head_dim, hipStream_t stream) {
+  DITK_REQUIRE(head_dim == 64, "ditk_joint_attn_q_prescaled: head_dim must be 64, got %d", head_dim);
+  DITK_REQUIRE(cu_a && cu_b, "ditk_joint_attn_q_prescaled: null segment table");
+  return flash_launch(q_a, ldq, k_a, ldk, vt, vt_ld, o_a, ldo, nullptr, 0, cu_joint, cu_joint, nseg, T_joint, heads,
+                      head_dim, 1.0f, true, stream, q_b, k_b, o_b, cu_a, cu_b);
 }

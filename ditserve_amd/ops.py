@@ -412,6 +412,67 @@ def joint_gather(img, txt, seg_img, seg_txt, out=None):
     return out
 
 
+def _joint_tables(seg_img, seg_txt, seg_joint):
+    if not (seg_img.nseg == seg_txt.nseg == seg_joint.nseg):
+        raise ValueError("image, text and joint segment tables must have the same number of segments")
+    if list(seg_joint.cu) != [int(a) + int(b) for a, b in zip(seg_img.cu, seg_txt.cu)]:
+        raise ValueError("joint segments must be cu_joint = cu_img + cu_txt")
+
+
+def transpose_v_joint(v_img, v_txt, heads, head_dim, seg_img, seg_txt, seg_joint):
+    """transpose_v of the joint rows (image rows of m, then text rows of m) read
+    straight from the two sources; the layout ditk_transpose_v gives the gathered V."""
+    _check(v_img, "v_img", _BF16, 2)
+    _check(v_txt, "v_txt", _BF16, 2)
+    _joint_tables(seg_img, seg_txt, seg_joint)
+    if v_img.shape != (seg_img.total, heads * head_dim) or v_txt.shape != (seg_txt.total, heads * head_dim):
+        raise ValueError("v_img / v_txt must be [segment total, heads*head_dim]")
+    ldv = _rows(v_img, "v_img")
+    if _rows(v_txt, "v_txt") != ldv:
+        raise ValueError("v_img and v_txt must share a row stride")
+    T = seg_joint.total
+    cols = vt_columns(T, seg_joint.nseg)
+    vt = torch.empty((heads, head_dim, cols), dtype=_BF16, device=v_img.device)
+    _lib.call("ditk_transpose_v_joint", _ptr(v_img), _ptr(v_txt), ldv, _ptr(vt), cols, T, heads, head_dim,
+              _ptr(seg_img.dev), _ptr(seg_txt.dev), _ptr(seg_joint.dev), seg_joint.nseg, _stream())
+    return vt
+
+
+def joint_attention_q_prescaled(q_img, q_txt, k_img, k_txt, vt, seg_img, seg_txt, seg_joint, heads, head_dim,
+                                out_img=None, out_txt=None):
+    """Joint attention straight from the image and text projections (head_dim 64,
+    q pre-scaled by softmax_scale * log2(e), vt from transpose_v_joint): joint
+    segment m = image rows of m, then text rows of m.  Returns (o_img, o_txt),
+    bitwise equal to joint_gather -> flash_attn_varlen(q_prescaled=True) ->
+    joint_scatter."""
+    width = heads * head_dim
+    if head_dim != 64:
+        raise ValueError("joint attention from two sources needs head_dim 64")
+    _joint_tables(seg_img, seg_txt, seg_joint)
+    for a, b, t in ((q_img, q_txt, "q"), (k_img, k_txt, "k")):
+        _check(a, t + "_img", _BF16, 2)
+        _check(b, t + "_txt", _BF16, 2)
+        if a.shape != (seg_img.total, width) or b.shape != (seg_txt.total, width):
+            raise ValueError(f"{t}_img / {t}_txt must be [segment total, {width}]")
+        if _rows(a, t + "_img") != _rows(b, t + "_txt"):
+            raise ValueError(f"{t}_img and {t}_txt must share a row stride")
+    T = seg_joint.total
+    _check(vt, "vt", _BF16, 3)
+    if vt.shape[:2] != (heads, head_dim) or not vt.is_contiguous() or vt.shape[2] < vt_columns(T, seg_joint.nseg):
+        raise ValueError("vt must be a contiguous [heads, head_dim, >= vt_columns(T_joint, nseg)] buffer")
+    if out_img is None:
+        out_img = torch.empty((seg_img.total, width), dtype=_BF16, device=q_img.device)
+    if out_txt is None:
+        out_txt = torch.empty((seg_txt.total, width), dtype=_BF16, device=q_img.device)
+    if _rows(out_img, "out_img") != _rows(out_txt, "out_txt"):
+        raise ValueError("out_img and out_txt must share a row stride")
+    _lib.call("ditk_joint_attn_q_prescaled", _ptr(q_img), _ptr(q_txt), _rows(q_img, "q_img"), _ptr(k_img),
+              _ptr(k_txt), _rows(k_img, "k_img"), _ptr(vt), vt.shape[2], _ptr(out_img), _ptr(out_txt),
+              _rows(out_img, "out_img"), _ptr(seg_img.dev), _ptr(seg_txt.dev), _ptr(seg_joint.dev),
+              seg_joint.nseg, T, heads, head_dim, _stream())
+    return out_img, out_txt
+
+
 def joint_scatter(joint, img, txt, seg_img, seg_txt):
     """Inverse of joint_gather: joint rows back into img / txt buffers."""
     total = seg_img.total + seg_txt.total

@@ -280,22 +280,32 @@ class SD35Transformer:
         with prof.region("gemm_qkv"):
             qkv_i = ops.linear(nh, *blk["qkv"])
             qkv_t = ops.linear(nc, *blk["qkv_t"])
+        pre = "_pre" if self._q_pre else ""
         with prof.region("joint_prep"):
             D3 = 3 * D
-            pre = "_pre" if self._q_pre else ""
             ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq" + pre], blk["nk"], cfg.head_dim, eps,
                               per_head=True)
             ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt" + pre], blk["nkt"], cfg.head_dim, eps,
                               per_head=True)
-            joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
-            vt = ops.transpose_v(joint[:, 2 * D:D3], cfg.heads, cfg.head_dim, seg_joint)
+            if self._q_pre:  # image and text rows read in place: no gather / scatter copies
+                vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
+                                           seg_img, seg_txt, seg_joint)
+            else:
+                joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
+                vt = ops.transpose_v(joint[:, 2 * D:D3], cfg.heads, cfg.head_dim, seg_joint)
         with prof.region("attn_joint"):
-            a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, seg_joint, seg_joint,
-                                      cfg.heads, cfg.head_dim, vt=vt, q_prescaled=self._q_pre)
-        with prof.region("joint_scatter"):
-            a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
-            a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
-            ops.joint_scatter(a, a_img, a_txt, seg_img, seg_txt)
+            if self._q_pre:
+                a_img, a_txt = ops.joint_attention_q_prescaled(
+                    qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D], vt, seg_img, seg_txt,
+                    seg_joint, cfg.heads, cfg.head_dim)
+            else:
+                a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, seg_joint, seg_joint,
+                                          cfg.heads, cfg.head_dim, vt=vt)
+        if not self._q_pre:
+            with prof.region("joint_scatter"):
+                a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
+                a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
+                ops.joint_scatter(a, a_img, a_txt, seg_img, seg_txt)
         with prof.region("gemm_out"):
             h = ops.linear(a_img, *blk["out"], "gate_res", residual=h, gate=emb[:, 2 * D:3 * D], segments=seg_img)
         if blk["dual"]:

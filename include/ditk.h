@@ -119,6 +119,31 @@ int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, const void* k
                                        int head_dim, ditk_stream_t stream);
 
 /*
+ * Joint attention over two packed sources, q pre-scaled as above (head_dim 64).
+ * Joint segment m is the rows [cu_a[m], cu_a[m+1]) of the "a" operands followed
+ * by the rows [cu_b[m], cu_b[m+1]) of the "b" operands (cu_joint = cu_a + cu_b);
+ * each attends to its own joint segment, and o_a / o_b receive the outputs of
+ * the a / b rows.  q_a, q_b share ldq; k_a, k_b share ldk; o_a, o_b share ldo.
+ * Bitwise equal to gathering the joint rows, ditk_flash_attn_varlen_q_prescaled,
+ * and scattering the result.  No reference counterpart: SD3.5's image (a) and
+ * text (b) streams enter joint attention without the gather the reference does
+ * (sd35_batch.py:230-317) and leave it without the scatter.
+ */
+int ditk_joint_attn_q_prescaled(const void* q_a, const void* q_b, int64_t ldq, const void* k_a, const void* k_b,
+                                int64_t ldk, const void* vt, int64_t vt_ld, void* o_a, void* o_b, int64_t ldo,
+                                const int32_t* cu_a, const int32_t* cu_b, const int32_t* cu_joint, int nseg,
+                                int T_joint, int heads, int head_dim, ditk_stream_t stream);
+
+/*
+ * ditk_transpose_v over the joint rows of two sources (v_a, v_b sharing ldv),
+ * laid out as ditk_transpose_v lays out the gathered joint V.  No reference
+ * counterpart (staging for ditk_joint_attn_q_prescaled).
+ */
+int ditk_transpose_v_joint(const void* v_a, const void* v_b, int64_t ldv, void* vt, int64_t vt_ld, int T_joint,
+                           int heads, int head_dim, const int32_t* cu_a, const int32_t* cu_b,
+                           const int32_t* cu_joint, int nseg, ditk_stream_t stream);
+
+/*
  * latent [C, F, H, W] bf16 -> patches [S, C*pt*ph*pw] bf16 (Conv3d weight order).
  * Replaces: the patch_embedding input gather — transformer_wan.py:328-329.
  */

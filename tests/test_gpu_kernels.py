@@ -357,6 +357,45 @@ def test_timestep_embedding_and_cfg():
     assert torch.allclose(out, u + 5.0 * (c - u), atol=1e-5)
 
 
+@pytest.mark.parametrize("img,txt", [([300, 4096], [77, 333]), ([64, 0, 130], [0, 40, 333]), ([1], [63]),
+                                     ([0, 100], [50, 0])])
+def test_joint_attention_two_sources_bitwise(img, txt):
+    """Joint attention read straight from the image and text buffers (and V transposed
+    from them) is bitwise the gather -> pre-scaled flash -> scatter path, including
+    segments without text or without image rows and tiles across the image/text seam."""
+    ops = _ops()
+    H, Dh, W = 4, 64, 3 * 4 * 64
+    cu_i, cu_t = [0], [0]
+    for a, b in zip(img, txt):
+        cu_i.append(cu_i[-1] + a)
+        cu_t.append(cu_t[-1] + b)
+    cu_j = [a + b for a, b in zip(cu_i, cu_t)]
+    g = torch.Generator(device=DEV).manual_seed(95)
+    qkv_i = (torch.randn((cu_i[-1], W), generator=g, device=DEV) * 0.3).to(torch.bfloat16)
+    qkv_t = (torch.randn((cu_t[-1], W), generator=g, device=DEV) * 0.3).to(torch.bfloat16)
+    si, st, sj = _seg(cu_i), _seg(cu_t), _seg(cu_j)
+    D = H * Dh
+    joint = ops.joint_gather(qkv_i, qkv_t, si, st)
+    vt_ref = ops.transpose_v(joint[:, 2 * D:], H, Dh, sj)
+    ref = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, sj, sj, H, Dh, vt=vt_ref, q_prescaled=True)
+    ref_i = torch.empty((cu_i[-1], D), dtype=torch.bfloat16, device=DEV)
+    ref_t = torch.empty((cu_t[-1], D), dtype=torch.bfloat16, device=DEV)
+    ops.joint_scatter(ref, ref_i, ref_t, si, st)
+    vt = ops.transpose_v_joint(qkv_i[:, 2 * D:], qkv_t[:, 2 * D:], H, Dh, si, st, sj)
+    used = sum(-(-(b - a) // 64) * 64 for a, b in zip(cu_j, cu_j[1:]))  # written columns; the rest is slack
+    assert torch.equal(vt[:, :, :used], vt_ref[:, :, :used])
+    o_i, o_t = ops.joint_attention_q_prescaled(qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D],
+                                               vt, si, st, sj, H, Dh)
+    assert torch.equal(o_i, ref_i) and torch.equal(o_t, ref_t)
+
+
+def test_joint_attention_rejects_inconsistent_tables():
+    ops = _ops()
+    x = torch.zeros((64, 256), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="cu_joint"):
+        ops.transpose_v_joint(x[:32], x[:32], 4, 64, _seg([0, 32]), _seg([0, 32]), _seg([0, 60]))
+
+
 def test_joint_gather_scatter_roundtrip():
     ops = _ops()
     img_counts, txt_counts = [40, 7, 100], [33, 33, 33]

@@ -25,7 +25,8 @@ def _seg(cu):
 
 # --------------------------------------------------------------------------- GEMM
 GEMM_CASES = [(1000, 1536, 1536), (256, 4608, 1536), (77, 64, 1536), (513, 384, 8960), (33, 1536, 64),
-              (300, 512, 96)]  # K % 64 == 32: the 32-k stage path
+              (300, 512, 96),  # K % 64 == 32: the 32-k stage path
+              (4000, 4104, 1536)]  # 16 x 17 = 272 256x256 tiles (the large configuration), ragged M and N
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)

@@ -136,94 +136,54 @@ __global__ void modulation_kernel(const float* __restrict__ table, const float* 
 // position on the axis that owns p: p < t_pairs -> frame, p < t_pairs+h_pairs
 // -> row, else column.  Angles come from cos/sin tables [max_pos][head_dim/2]
 // built in float64 and rounded to fp32 on the host.
-// Work item: one wave per (token, tensor) with tensor 0 = q, 1 = k.
+// Work item: one wave per token, normalising its q row and its k row, so the
+// segment search, the position arithmetic and the rotation's table loads are
+// shared by both.  Every address computation stays in registers (positions are
+// selected by value), so the kernel uses no scratch or LDS.
 // ---------------------------------------------------------------------------
-template <int GROUP_LANES, int NC>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
-    bf16_t* __restrict__ q, int64_t ldq, bf16_t* __restrict__ k, int64_t ldk, int T, int D,
-    int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
-    const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
-    int h_pairs) {
-  const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (item >= 2 * T) return;
-  const int row = item >> 1;
-  const int which = item & 1;
-  bf16_t* xr = which ? (k + (int64_t)row * ldk) : (q + (int64_t)row * ldq);
-  const float* w = which ? wk : wq;
-  const int nchunk = D >> 3;
-  // Every load is issued before the reduction: the row (kept packed), the
-  // norm weights and, with RoPE, the table entries of the token's positions.
-  u32x4_t raw[NC];
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = i * 64 + lane;
-    raw[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(xr + c * 8) : u32x4_t{0, 0, 0, 0};
-  }
-  f32x4_t w4[NC][2];
+template <int NC>
+__device__ __forceinline__ void load_w(const float* __restrict__ w, int nchunk, int lane, f32x4_t (&w4)[NC][2]) {
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = min(i * 64 + lane, nchunk - 1);
     w4[i][0] = *reinterpret_cast<const f32x4_t*>(w + c * 8);
     w4[i][1] = *reinterpret_cast<const f32x4_t*>(w + c * 8 + 4);
   }
-  // RoPE: chunk c holds pairs p0..p0+3 of its head, p0 = 4 * (c % (head_dim/8));
-  // with 64 lanes per chunk row that is the same quad for every chunk of a lane,
-  // so each lane loads its rotation once.  The quad's pairs belong to at most
-  // two axes: table entries of the axis of the first pair and of the last pair.
-  const bool rope = rcos != nullptr;
-  const int p0 = (lane % (head_dim >> 3)) * 4;
-  float rc[4], rsn[4];
-  if (rope) {
-    const int half = head_dim >> 1;
-    const int seg = find_segment(cu, nseg, row);
-    const int s = row - cu[seg];
-    const int gh = grids[seg * 3 + 1], gw = grids[seg * 3 + 2];
-    const int pf = min(s / (gh * gw), max_pos - 1);
-    const int ph = min((s / gw) % gh, max_pos - 1);
-    const int pw = min(s % gw, max_pos - 1);
-    auto axis_pos = [&](int p) { return p < t_pairs ? pf : (p < t_pairs + h_pairs ? ph : pw); };
-    const int pa = axis_pos(p0), pb = axis_pos(p0 + 3);
-    const f32x4_t ca = *reinterpret_cast<const f32x4_t*>(rcos + pa * half + p0);
-    const f32x4_t sa = *reinterpret_cast<const f32x4_t*>(rsin + pa * half + p0);
-    f32x4_t cb = ca, sb = sa;
-    if (pb != pa) {
-      cb = *reinterpret_cast<const f32x4_t*>(rcos + pb * half + p0);
-      sb = *reinterpret_cast<const f32x4_t*>(rsin + pb * half + p0);
-    }
+}
+
+// reciprocal RMS of each chunk's group (one value per chunk; equal across a
+// wave when the group is the whole row)
+template <int GROUP_LANES, int NC>
+__device__ __forceinline__ void group_rstd(const u32x4_t (&raw)[NC], int D, int head_dim, float eps,
+                                           float (&rs)[NC]) {
+  float ss[NC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool first = (p0 + j < t_pairs) == (p0 < t_pairs) &&
-                         (p0 + j < t_pairs + h_pairs) == (p0 < t_pairs + h_pairs);
-      rc[j] = first ? ca[j] : cb[j];
-      rsn[j] = first ? sa[j] : sb[j];
-    }
+  for (int i = 0; i < NC; ++i) {
+    float v[8];
+    unpack8(raw[i], v);
+    ss[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss[i] = fmaf(v[j], v[j], ss[i]);
   }
-  float rs[NC];
-  {
-    float ss[NC];
+  if (GROUP_LANES == 64) {
+    float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      float v[8];
-      unpack8(raw[i], v);
-      ss[i] = 0.f;
+    for (int i = 0; i < NC; ++i) t += ss[i];
+    const float r = rsqrtf(wave_sum<64>(t) / (float)D + eps);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss[i] = fmaf(v[j], v[j], ss[i]);
-    }
-    if (GROUP_LANES == 64) {
-      float t = 0.f;
+    for (int i = 0; i < NC; ++i) rs[i] = r;
+  } else {
+    // a head spans GROUP_LANES consecutive lanes of one chunk row
 #pragma unroll
-      for (int i = 0; i < NC; ++i) t += ss[i];
-      const float r = rsqrtf(wave_sum<64>(t) / (float)D + eps);
-#pragma unroll
-      for (int i = 0; i < NC; ++i) rs[i] = r;
-    } else {
-      // a head spans GROUP_LANES consecutive lanes of one chunk row
-#pragma unroll
-      for (int i = 0; i < NC; ++i) rs[i] = rsqrtf(wave_sum<GROUP_LANES>(ss[i]) / (float)head_dim + eps);
-    }
+    for (int i = 0; i < NC; ++i) rs[i] = rsqrtf(wave_sum<GROUP_LANES>(ss[i]) / (float)head_dim + eps);
   }
+}
+
+template <int NC>
+__device__ __forceinline__ void norm_rotate_store(bf16_t* __restrict__ xr, const u32x4_t (&raw)[NC],
+                                                  const float (&rs)[NC], const f32x4_t (&w4)[NC][2],
+                                                  bool rope, const float (&rc)[4], const float (&rsn)[4],
+                                                  int nchunk, int lane) {
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = i * 64 + lane;
@@ -246,6 +206,76 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       *reinterpret_cast<u32x4_t*>(xr + c * 8) = pack8(o);
     }
   }
+}
+
+template <int GROUP_LANES, int NC>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    bf16_t* __restrict__ q, int64_t ldq, bf16_t* __restrict__ k, int64_t ldk, int T, int D,
+    int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
+    const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
+    int h_pairs) {
+  // Norm weights are L2-resident; up to 4 chunks per lane they are loaded with
+  // the rows (before the reductions), above that after them to bound registers.
+  constexpr bool kEarlyW = NC <= 4;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= T) return;
+  bf16_t* qr = q + (int64_t)row * ldq;
+  bf16_t* kr = k + (int64_t)row * ldk;
+  const int nchunk = D >> 3;
+  u32x4_t rawq[NC], rawk[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = i * 64 + lane;
+    rawq[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(qr + c * 8) : u32x4_t{0, 0, 0, 0};
+    rawk[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(kr + c * 8) : u32x4_t{0, 0, 0, 0};
+  }
+  f32x4_t wq4[NC][2], wk4[NC][2];
+  if (kEarlyW) {
+    load_w<NC>(wq, nchunk, lane, wq4);
+    load_w<NC>(wk, nchunk, lane, wk4);
+  }
+  // RoPE: chunk c holds pairs p0..p0+3 of its head, p0 = 4 * (c % (head_dim/8));
+  // with 64 lanes per chunk row that is the same quad for every chunk of a lane,
+  // so each lane loads its rotation once, for q and k together.  The quad's
+  // pairs belong to at most two axes: table entries of the axis of the first
+  // pair and of the last pair.
+  const bool rope = rcos != nullptr;
+  const int p0 = (lane % (head_dim >> 3)) * 4;
+  float rc[4] = {1.f, 1.f, 1.f, 1.f}, rsn[4] = {0.f, 0.f, 0.f, 0.f};
+  if (rope) {
+    const int half = head_dim >> 1;
+    const int seg = find_segment(cu, nseg, row);
+    const int s = row - cu[seg];
+    const int gh = grids[seg * 3 + 1], gw = grids[seg * 3 + 2];
+    const int pf = min(s / (gh * gw), max_pos - 1);
+    const int ph = min((s / gw) % gh, max_pos - 1);
+    const int pw = min(s % gw, max_pos - 1);
+    const int th = t_pairs + h_pairs;
+    const int pa = p0 < t_pairs ? pf : (p0 < th ? ph : pw);
+    const int pb = p0 + 3 < t_pairs ? pf : (p0 + 3 < th ? ph : pw);
+    const f32x4_t ca = *reinterpret_cast<const f32x4_t*>(rcos + pa * half + p0);
+    const f32x4_t sa = *reinterpret_cast<const f32x4_t*>(rsin + pa * half + p0);
+    const f32x4_t cb = *reinterpret_cast<const f32x4_t*>(rcos + pb * half + p0);
+    const f32x4_t sb = *reinterpret_cast<const f32x4_t*>(rsin + pb * half + p0);
+    const bool a_t = p0 < t_pairs, a_h = p0 < th;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool first = ((p0 + j < t_pairs) == a_t) && ((p0 + j < th) == a_h);
+      rc[j] = first ? ca[j] : cb[j];
+      rsn[j] = first ? sa[j] : sb[j];
+    }
+  }
+  float rsq[NC], rsk[NC];
+  group_rstd<GROUP_LANES, NC>(rawq, D, head_dim, eps, rsq);
+  group_rstd<GROUP_LANES, NC>(rawk, D, head_dim, eps, rsk);
+  if (!kEarlyW) {
+    load_w<NC>(wq, nchunk, lane, wq4);
+    load_w<NC>(wk, nchunk, lane, wk4);
+  }
+  norm_rotate_store<NC>(qr, rawq, rsq, wq4, rope, rc, rsn, nchunk, lane);
+  norm_rotate_store<NC>(kr, rawk, rsk, wk4, rope, rc, rsn, nchunk, lane);
 }
 
 }  // namespace
@@ -323,7 +353,7 @@ DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, in
   DITK_REQUIRE(rope_cos == nullptr || (((uintptr_t)rope_cos % 16) == 0 && ((uintptr_t)rope_sin % 16) == 0),
                "ditk_qk_norm_rope: RoPE tables must be 16-byte aligned");
   if (T == 0) return 0;
-  dim3 grid((2 * T + kRowsPerBlock - 1) / kRowsPerBlock);
+  dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
 #define DITK_QKN(G, NCV)                                                                                  \
   qk_norm_rope_kernel<G, NCV><<<grid, 256, 0, stream>>>((bf16_t*)q, ldq, (bf16_t*)k, ldk, T, D, head_dim, \

@@ -1,19 +1,32 @@
 #!/usr/bin/env python3
 """Benchmark: one Wan2.1-T2V-1.3B denoise step at 480x832x81 frames with CFG batch 2
-(2 x 32760 tokens), bf16, on one MI355X.
+(2 x 32760 tokens), bf16, on one MI355X -- plus the other single-GPU workloads of
+the same path, each measured in the same run and reported under ``per_config``.
 
-A step = packed prelude for the (cond, uncond) pair + 30 DiT blocks + prediction
-+ the fused CFG combine and UniPC update (Wan's scheduler recipe: flow sigmas,
-shift 3.0, 50-step schedule, order 2 with corrector), all on the ditk HIP kernels.
-The model timestep of each step is the schedule's (999, 997, ...).
+Headline step = packed prelude for the (cond, uncond) pair + 30 DiT blocks +
+prediction + the fused CFG combine and UniPC update (Wan's scheduler recipe: flow
+sigmas, shift 3.0, 50-step schedule, order 2 with corrector), all on the ditk HIP
+kernels.  The model timestep of each step is the schedule's (999, 997, ...).
 Synthetic data: random-init weights N(0, 0.02^2) (norm weights N(1, 0.02^2)),
 latent 16x21x60x104 N(0,1), text contexts 512x4096 N(0,1) with 120 (cond) and 0
 (uncond) valid rows.
 
-Prints one JSON line (rank 0).  `roofline` is for the dominant kernel, the
-self-attention flash kernel, from HIP events recorded on its launch stream over
-the timed steps.  `cpu_baseline` times the oracle (CPU fp32 restatement of the
-reference block) on one full-shape block-forward and extrapolates x60.
+``per_config`` adds, each with its own steps/s (or forwards/s), tokens/s,
+attention roofline fraction and CPU baseline:
+  * wan21_block_1560tok   one Wan2.1 block, 1x30x52 grid (1560 tokens), 77 valid
+                          text rows, t = 500 (GPU bf16 vs the oracle in fp32 on CPU);
+  * wan21_packed_4req     four requests packed into one varlen batch (grids 21x30x52,
+                          9x30x52, 13x20x32, 5x16x16 = 56400 tokens), own timesteps
+                          U[0,1000) and texts (valid 30-200): one packed forward;
+  * sd35_medium_1024_cfg2 SD3.5-Medium 1024^2 step, CFG pair of joint segments
+                          (4096 image + 333 text tokens each), FlowMatch-Euler;
+  * wan22_ti2v_5b_704p_cfg2  Wan2.2-TI2V-5B 704x1280x121f step, CFG pair of
+                          2 x 27280 tokens, text valid 150/0, t = 700 schedule.
+
+Prints one JSON line.  ``roofline`` is for the dominant kernel, the self-attention
+flash kernel, from HIP events recorded on its launch stream over the timed steps.
+``cpu_baseline`` times the oracle (the CPU fp32 restatement of the reference block)
+on one full-shape block-forward and extrapolates to the step (blocks x branches).
 """
 import argparse
 import json
@@ -21,29 +34,31 @@ import os
 import sys
 import time
 
-METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0
-LATENT = (16, 21, 60, 104)
-TEXT_VALID = (120, 0)
-GUIDANCE = 5.0
-FLOW_SHIFT = 3.0
-SCHEDULE_STEPS = 50
 CALIB_BYTES = 256 << 20
-# A100-PCIe-40GB, fp16, same workload: 3964.62 ms per step (the reference's published figure)
-REFERENCE_STEPS_PER_S = 1000.0 / 3964.62
-# HBM traffic of one self-attention launch, from two rocprofv3 --pmc passes over this
-# bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that counter's
-# reading for the CALIB_BYTES copy: FETCH 917467.5 KiB x 1.9997, WRITE 196581.8 KiB x 1.0000
-# (profiles/wan21_480p_cfg2_step_traffic.md).  Re-measure after kernel changes.
+GUIDANCE = 5.0
+SCHEDULE_STEPS = 50
+# HBM traffic of one headline self-attention launch, from two rocprofv3 --pmc passes
+# over this bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that
+# counter's reading for the CALIB_BYTES copy: FETCH 917467.5 KiB x 1.9997, WRITE
+# 196581.8 KiB x 1.0000 (profiles/wan21_480p_cfg2_step_traffic.md).
 ATTN_SELF_TRAFFIC_BYTES = (917548 * 1.9997 + 196607 * 1.0000) * 1024
 
-
-# Other single-GPU workloads of the same step (reported per config; the default
-# line is the headline): A100-PCIe reference step times for the same shapes.
+WAN21_METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFMA peak"
 WORKLOADS = {
-    "wan21_480p": None,
-    "wan22_ti2v_5b_704p": dict(latent=(48, 31, 44, 80), text_valid=(150, 0), flow_shift=5.0, ref_ms=7813.18),
-    "sd35_medium_1024": dict(latent=(16, 128, 128), text_len=333, steps=28, shift=3.0, ref_ms=217.23),
+    "wan21_480p": dict(
+        metric=WAN21_METRIC, arch="wan21", latent=(16, 21, 60, 104), text_valid=(120, 0), flow_shift=3.0,
+        ref_ms=3964.62),
+    "wan22_ti2v_5b_704p": dict(
+        metric="denoise steps/s & tokens/s, Wan2.2-TI2V-5B 704p-121f CFG2; attn % bf16 MFMA peak",
+        arch="wan22", latent=(48, 31, 44, 80), text_valid=(150, 0), flow_shift=5.0, ref_ms=7813.18),
+    "sd35_medium_1024": dict(
+        metric="denoise steps/s & tokens/s, SD3.5-Medium 1024x1024 CFG2; joint attn % bf16 MFMA peak",
+        latent=(16, 128, 128), text_len=333, steps=28, shift=3.0, ref_ms=217.23),
+    "wan21_packed_4req": dict(
+        metric="packed forwards/s & tokens/s, Wan2.1-1.3B 4-request varlen batch (56400 tokens); "
+               "attn % bf16 MFMA peak",
+        shapes=[(16, 21, 60, 104), (16, 9, 60, 104), (16, 13, 40, 64), (16, 5, 32, 32)]),
 }
 
 
@@ -53,173 +68,315 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-config", action="store_true", help="headline workload only")
     ap.add_argument("--breakdown", action="store_true", help="per-op HIP-event breakdown in the JSON")
     ap.add_argument("--workload", default="wan21_480p", choices=sorted(WORKLOADS),
-                    help="wan21_480p (the headline line), wan22_ti2v_5b_704p or sd35_medium_1024")
+                    help="the workload of the top-level line (default: the Wan2.1 480p headline)")
     return ap.parse_args()
 
 
-def cpu_baseline(seq=32760, grid=(21, 30, 52)):
-    """Oracle (CPU fp32, the reference block arithmetic on PyTorch CPU ops) on one
-    full-shape Wan2.1 block-forward; steps/s extrapolated over 30 blocks x 2 branches."""
+# ---------------------------------------------------------------------------
+# CPU baselines: the oracle (CPU fp32 restatement of the reference arithmetic)
+# ---------------------------------------------------------------------------
+
+def cpu_threads():
+    """Threads for the CPU baseline: the host's cores, bounded by the CPUs this
+    process may run on and by OMP_NUM_THREADS when the environment sets it."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:  # pragma: no cover
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
+
+
+def _cpu_info(threads, kind="port"):
+    return {"cores": threads, "threads": threads, "host_cores": os.cpu_count(), "kind": kind}
+
+
+def cpu_wan_block_s(cfg, seqs, text_len=512, seed=0):
+    """Seconds for one oracle Wan block-forward over `seqs` (a packed batch when
+    several), fp32, torch's CPU flash SDPA.  A warm-up on a small slice first."""
     import torch
 
     from ditserve_amd.wan import WanConfig, random_state_dict
     from oracle import common as oc
     from oracle import wan as ow
 
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    cfg = WanConfig(layers=1)
-    sd = random_state_dict(cfg, seed=0)
-    g = torch.Generator().manual_seed(2)
-    h = torch.randn(seq, cfg.dim, generator=g)
-    enc = torch.randn(cfg.text_len, cfg.dim, generator=g)
-    proj = torch.randn(6, cfg.dim, generator=g) * 0.02
-    cos, sin = ow.rope_freqs(grid)
-    # warm-up on a small slice, then one timed full-shape block
-    ow.block_forward(sd, 0, h[:1560], enc, proj, cos[:1560], sin[:1560], cfg.heads, attn=oc.sdpa_fast)
+    one = WanConfig(**{**cfg.as_dict(), "layers": 1})
+    sd = random_state_dict(one, seed=seed)
+    g = torch.Generator().manual_seed(seed + 2)
+    grids = [s for s in seqs]
+    counts = [f * h * w for f, h, w in grids]
+    h = torch.randn(sum(counts), cfg.dim, generator=g)
+    encs = [torch.randn(text_len, cfg.dim, generator=g) for _ in counts]
+    projs = torch.randn(len(counts), 6, cfg.dim, generator=g) * 0.02
+    rot = [ow.rope_freqs(gr, cfg.head_dim) for gr in grids]
+    w = min(counts[0], 1560)
+    ow.block_forward(sd, 0, h[:w], encs[0], projs[0], rot[0][0][:w], rot[0][1][:w], cfg.heads, attn=oc.sdpa_fast)
+    cu = [0]
+    for n in counts:
+        cu.append(cu[-1] + n)
     t0 = time.perf_counter()
-    ow.block_forward(sd, 0, h, enc, proj, cos, sin, cfg.heads, attn=oc.sdpa_fast)
-    block_s = time.perf_counter() - t0
-    step_s = block_s * cfg.layers * 2
-    return {
-        "value": 1.0 / step_s,
-        "unit": "steps/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"1 Wan2.1 block-forward at S={seq} (one CFG branch), fp32, CPU flash SDPA: "
-                  f"{block_s:.2f} s; extrapolated x60 (30 blocks x 2 branches)",
-        "tokens_per_s": 2 * seq / step_s,
-    }
+    ow.block_forward_packed(sd, 0, h, cu, encs, projs, rot, cfg.heads, attn=oc.sdpa_fast)
+    return time.perf_counter() - t0
 
 
-def main():
-    args = parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); this build "
-              "has no multi-GPU path", file=sys.stderr)
-        sys.exit(2)
+def cpu_baseline_wan_step(cfg, grid, threads, label):
+    """configs with a CFG pair: one block-forward at the full shape (one branch),
+    extrapolated x (layers x 2 branches)."""
+    s = cpu_wan_block_s(cfg, [grid])
+    seq = grid[0] * grid[1] * grid[2]
+    step_s = s * cfg.layers * 2
+    return dict(value=1.0 / step_s, unit="steps/s", tokens_per_s=2 * seq / step_s, block_s=s,
+                sample=f"1 {label} block-forward at S={seq} (one CFG branch), fp32, CPU flash SDPA, {threads} "
+                       f"threads: {s:.2f} s; extrapolated x{cfg.layers * 2} ({cfg.layers} blocks x 2 branches)",
+                **_cpu_info(threads))
 
-    if args.workload == "sd35_medium_1024":
-        return run_sd35(args)
 
+def cpu_baseline_wan_packed(cfg, grids, threads):
+    s = cpu_wan_block_s(cfg, grids)
+    tokens = sum(f * h * w for f, h, w in grids)
+    fwd_s = s * cfg.layers
+    return dict(value=1.0 / fwd_s, unit="forwards/s", tokens_per_s=tokens / fwd_s, block_s=s,
+                sample=f"1 Wan2.1 block-forward over the 4-request packed batch ({tokens} tokens, per-segment CPU "
+                       f"flash SDPA), fp32, {threads} threads: {s:.2f} s; extrapolated x{cfg.layers} blocks",
+                **_cpu_info(threads))
+
+
+def cpu_baseline_wan_block(cfg, threads, repeats=5):
+    """One Wan2.1 block on the 1x30x52 grid: 2 warm-ups, median of `repeats`."""
+    import torch
+
+    from ditserve_amd.wan import WanConfig, random_state_dict
+    from oracle import wan as ow
+
+    one = WanConfig(**{**cfg.as_dict(), "layers": 1})
+    sd = random_state_dict(one, seed=0)
+    g = torch.Generator().manual_seed(2)
+    h = torch.randn(1560, cfg.dim, generator=g)
+    enc = torch.randn(512, cfg.dim, generator=g)
+    enc[77:] = 0
+    proj = torch.randn(6, cfg.dim, generator=g) * 0.02
+    cos, sin = ow.rope_freqs((1, 30, 52))
+    times = []
+    for i in range(2 + repeats):
+        t0 = time.perf_counter()
+        ow.block_forward(sd, 0, h, enc, proj, cos, sin, cfg.heads)
+        if i >= 2:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return dict(value=1000.0 * med, unit="ms/block", block_s=med,
+                sample=f"Wan2.1 block, 1560 tokens, 512 text rows, fp32 (oracle's exact SDPA), {threads} threads: "
+                       f"median of {repeats} after 2 warm-ups", **_cpu_info(threads))
+
+
+def cpu_baseline_sd35(cfg, n_img, text_len, threads):
+    """One dual-attention and one plain SD3.5 joint block on one CFG branch
+    (n_img image + text_len text tokens), extrapolated to the step:
+    2 branches x (dual x 13 + plain x 11) -- the last block, which drops its
+    text stream, is counted as plain."""
+    import torch
+
+    from ditserve_amd.sd35 import SD35Config, random_state_dict
+    from oracle import common as oc
+    from oracle import sd35 as osd
+
+    two = SD35Config(**{**cfg.__dict__, "layers": 3, "dual_layers": (0,)})
+    sd = random_state_dict(two, seed=0)
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(n_img, cfg.dim, generator=g)
+    c = torch.randn(text_len, cfg.dim, generator=g)
+    temb = torch.randn(cfg.dim, generator=g)
+    ocfg = dict(heads=cfg.heads, eps=cfg.eps, layers=3, dual_layers=(0,))
+    osd.joint_block(sd, 1, h[:256], c[:32], temb, ocfg, attn=oc.sdpa_fast)  # warm-up
+    times = {}
+    for name, i in (("dual", 0), ("plain", 1)):
+        t0 = time.perf_counter()
+        osd.joint_block(sd, i, h, c, temb, ocfg, attn=oc.sdpa_fast)
+        times[name] = time.perf_counter() - t0
+    n_dual = len(cfg.dual_layers)
+    step_s = 2 * (times["dual"] * n_dual + times["plain"] * (cfg.layers - n_dual))
+    return dict(value=1.0 / step_s, unit="steps/s", tokens_per_s=2 * n_img / step_s, dual_block_s=times["dual"],
+                plain_block_s=times["plain"],
+                sample=f"1 dual + 1 plain SD3.5-M joint block ({n_img} image + {text_len} text tokens, one CFG "
+                       f"branch), fp32, CPU flash SDPA, {threads} threads: {times['dual']:.2f} s + "
+                       f"{times['plain']:.2f} s; extrapolated x2 branches x ({n_dual} dual + "
+                       f"{cfg.layers - n_dual} plain blocks)", **_cpu_info(threads))
+
+
+# ---------------------------------------------------------------------------
+# GPU workloads
+# ---------------------------------------------------------------------------
+
+def _roofline(kernel, flops_per_launch, region, traffic=None, algorithmic_bytes=None):
+    tflops = flops_per_launch / (region["avg_ms"] * 1e-3) / 1e12
+    out = {"kernel": kernel, "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+           "frac": tflops / PEAK_BF16_TFLOPS, "traffic": traffic, "avg_launch_ms": region["avg_ms"],
+           "launches": region["count"], "flops_per_launch": flops_per_launch}
+    if traffic is not None:
+        out["traffic_unit"] = "bytes/launch"
+    if algorithmic_bytes is not None:
+        out["algorithmic_bytes"] = algorithmic_bytes
+    return out
+
+
+def _timed(step, state, steps, warmup, prof_model, only, breakdown):
+    """Run warmup + timed steps; returns (state, ms per step, region summary)."""
     import torch
 
     from ditserve_amd.profiling import EventProfiler
+
+    for _ in range(warmup):
+        state = step(state)
+    torch.cuda.synchronize()
+    prof = EventProfiler(enabled=True, only=None if breakdown else only)
+    prof_model.profiler = prof
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        state = step(state)
+    end.record()
+    torch.cuda.synchronize()
+    prof_model.profiler = EventProfiler(enabled=False)
+    return state, start.elapsed_time(end) / steps, prof.summary()
+
+
+def _release():
+    """Return the previous workload's device memory before the next one starts."""
+    import gc
+
+    import torch
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
+    """Wan CFG-pair denoise step (Wan2.1 480p or Wan2.2-5B 704p)."""
+    import torch
+
     from ditserve_amd.solver import UniPCFlowScheduler
     from ditserve_amd.wan import WAN21_T2V_1_3B, WAN22_TI2V_5B, WanTransformer, step_flops
 
-    wl = WORKLOADS[args.workload]
-    cfg = WAN21_T2V_1_3B if wl is None else WAN22_TI2V_5B
-    latent_shape = LATENT if wl is None else wl["latent"]
-    text_valid = TEXT_VALID if wl is None else wl["text_valid"]
-    flow_shift = FLOW_SHIFT if wl is None else wl["flow_shift"]
-    ref_steps_per_s = REFERENCE_STEPS_PER_S if wl is None else 1000.0 / wl["ref_ms"]
+    wl = WORKLOADS[name]
+    cfg = WAN21_T2V_1_3B if wl["arch"] == "wan21" else WAN22_TI2V_5B
+    latent_shape = wl["latent"]
     dev = "cuda"
     model = WanTransformer.random(cfg, seed=0, device=dev)
     g = torch.Generator(device=dev).manual_seed(1)
     latent = torch.randn(latent_shape, generator=g, device=dev)
     texts = []
-    for valid in text_valid:
+    for valid in wl["text_valid"]:
         t = torch.randn((cfg.text_len, cfg.text_dim), generator=g, device=dev)
         t[valid:] = 0
         texts.append(t)
-    seq = (latent_shape[1] // cfg.patch[0]) * (latent_shape[2] // cfg.patch[1]) * (latent_shape[3] // cfg.patch[2])
-    # calibration buffers for HBM-traffic counters: a plain copy of exactly
-    # CALIB_BYTES, run once after the timed steps (cold by then), outside timing
-    calib_src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
-    calib_dst = torch.empty_like(calib_src)
-
-    sched = UniPCFlowScheduler(flow_shift=flow_shift)
-    sched.set_timesteps(max(SCHEDULE_STEPS, args.warmup + args.steps))
+    pt, ph, pw = cfg.patch
+    grid = (latent_shape[1] // pt, latent_shape[2] // ph, latent_shape[3] // pw)
+    seq = grid[0] * grid[1] * grid[2]
+    sched = UniPCFlowScheduler(flow_shift=wl["flow_shift"])
+    sched.set_timesteps(max(SCHEDULE_STEPS, warmup + steps))
 
     def step(lat):
         t = float(sched.timesteps[sched.step_index])
         cond, uncond = model.forward_packed([lat, lat], [t, t], texts)
         return sched.step(cond, t, lat, uncond=uncond, guidance=GUIDANCE)[0]
 
-    for _ in range(args.warmup):
-        latent = step(latent)
-    torch.cuda.synchronize()
-
-    # only the roofline kernel's region is timed unless the breakdown is asked for
-    prof = EventProfiler(enabled=True, only=None if args.breakdown else {"attn_self"})
-    model.profiler = prof
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        latent = step(latent)
-    end.record()
-    torch.cuda.synchronize()
-    model.profiler = EventProfiler(enabled=False)
+    latent, ms, regions = _timed(step, latent, steps, warmup, model, {"attn_self"}, breakdown)
     if not bool(torch.isfinite(latent).all()):
-        raise RuntimeError("non-finite latent after the timed steps")
-    calib_dst.copy_(calib_src)  # the known-size copy the traffic counters are scaled by
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    regions = prof.summary()
-
-    attn = regions["attn_self"]
+        raise RuntimeError(f"{name}: non-finite latent after the timed steps")
+    if calibrate:
+        # the known-size copy the HBM-traffic counters are scaled by (outside timing)
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
     attn_flops = 4.0 * 2 * seq * seq * cfg.dim  # per launch: 2 segments (CFG pair), non-causal
-    attn_tflops = attn_flops / (attn["avg_ms"] * 1e-3) / 1e12
     total_flops = step_flops(cfg, [seq, seq], cfg.text_len)
-
+    arch = "Wan2.1-T2V-1.3B" if wl["arch"] == "wan21" else "Wan2.2-TI2V-5B"
+    frames = "480x832x81f" if wl["arch"] == "wan21" else "704x1280x121f"
     out = {
-        "metric": METRIC,
-        "value": 1000.0 / ms,
-        "unit": "steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": (1000.0 / ms) / ref_steps_per_s,
-        "dtype": "bf16",
-        "data": "synthetic: random-init weights N(0,0.02^2), latent/text N(0,1)",
-        "config": {"workload": (
-                       "Wan2.1-T2V-1.3B-architecture denoise step, latent 16x21x60x104 (480x832x81f), "
-                       "CFG pair packed as 2 x 32760 tokens, 30 blocks, text 512 (valid 120/0), UniPC flow-shift-3 "
-                       "50-step schedule (t = 999, 997, ...)") if wl is None else (
-                       f"Wan2.2-TI2V-5B-architecture denoise step, latent {'x'.join(map(str, latent_shape))} "
-                       f"(704x1280x121f), CFG pair packed as 2 x {seq} tokens, {cfg.layers} blocks, text 512 "
-                       f"(valid {text_valid[0]}/{text_valid[1]}), UniPC flow-shift-{flow_shift:g} 50-step schedule"),
-                   "tokens_per_step": 2 * seq, "blocks": cfg.layers},
-        "tokens_per_s": 2 * seq * 1000.0 / ms,
+        "metric": wl["metric"], "value": 1000.0 / ms, "unit": "steps/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "tokens_per_s": 2 * seq * 1000.0 / ms,
+        "workload": (f"{arch}-architecture denoise step, latent {'x'.join(map(str, latent_shape))} ({frames}), "
+                     f"CFG pair packed as 2 x {seq} tokens, {cfg.layers} blocks, text 512 (valid "
+                     f"{wl['text_valid'][0]}/{wl['text_valid'][1]}), UniPC flow-shift-{wl['flow_shift']:g} "
+                     f"{SCHEDULE_STEPS}-step schedule"),
+        "tokens_per_step": 2 * seq, "blocks": cfg.layers,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-        "roofline": {
-            "kernel": f"flash_fwd_kernel<128> (self-attention, 2 x {seq} tokens x {cfg.heads} heads)",
-            "bound": "mfma",
-            "achieved": attn_tflops,
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": attn_tflops / PEAK_BF16_TFLOPS,
-            "traffic": ATTN_SELF_TRAFFIC_BYTES if wl is None else None,
-            "traffic_unit": "bytes/launch",
-            "algorithmic_bytes": 4.0 * 2 * seq * cfg.dim * 2,
-            "avg_launch_ms": attn["avg_ms"],
-            "launches": attn["count"],
-            "flops_per_launch": attn_flops,
-        },
-        "reference_a100_steps_per_s": ref_steps_per_s,
+        "roofline": _roofline(f"flash_fwd_kernel<128> (self-attention, 2 x {seq} tokens x {cfg.heads} heads)",
+                              attn_flops, regions["attn_self"],
+                              ATTN_SELF_TRAFFIC_BYTES if name == "wan21_480p" else None,
+                              4.0 * 2 * seq * cfg.dim * 2),
+        "reference_a100_ms_per_step": wl["ref_ms"], "vs_reference_a100": wl["ref_ms"] / ms,
+        "_grid": grid, "_cfg": cfg,
     }
-    if args.breakdown:
-        out["breakdown_ms_per_step"] = {k: v["total_ms"] / args.steps for k, v in regions.items()}
-    if not args.no_cpu_baseline and wl is None:
-        out["cpu_baseline"] = cpu_baseline(seq)
-    print(json.dumps(out), flush=True)
+    if breakdown:
+        out["breakdown_ms_per_step"] = {k: v["total_ms"] / steps for k, v in regions.items()}
+    return out
 
 
-def run_sd35(args):
-    """SD3.5-Medium 1024^2 denoise step, CFG as a packed pair of joint
-    segments (4096 image + 333 text tokens each), 24 blocks, FlowMatch-Euler."""
+def run_wan_packed(steps, warmup, breakdown=False):
+    """Four Wan2.1 requests packed into one varlen batch: one packed forward
+    (prelude, 30 blocks, prediction) per step."""
     import torch
 
-    from ditserve_amd.profiling import EventProfiler
+    from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer, step_flops
+
+    wl = WORKLOADS["wan21_packed_4req"]
+    cfg, dev = WAN21_T2V_1_3B, "cuda"
+    model = WanTransformer.random(cfg, seed=4, device=dev)
+    g = torch.Generator().manual_seed(5)
+    lats = [torch.randn(s, generator=g).to(dev) for s in wl["shapes"]]
+    ts = [float(x) for x in (torch.rand(4, generator=g) * 1000)]
+    valid = [int(x) for x in torch.randint(30, 201, (4,), generator=g)]
+    texts = []
+    for i in range(4):
+        t = torch.randn((cfg.text_len, cfg.text_dim), generator=g)
+        t[valid[i]:] = 0
+        texts.append(t.to(dev))
+    grids = [(s[1], s[2] // 2, s[3] // 2) for s in wl["shapes"]]
+    seqs = [f * h * w for f, h, w in grids]
+
+    def step(_):
+        return model.forward_packed(lats, ts, texts)
+
+    outs, ms, regions = _timed(step, None, steps, warmup, model, {"attn_self"}, breakdown)
+    if not all(bool(torch.isfinite(o).all()) for o in outs):
+        raise RuntimeError("packed Wan forward produced non-finite values")
+    attn_flops = 4.0 * sum(s * s for s in seqs) * cfg.dim
+    total_flops = step_flops(cfg, seqs, cfg.text_len)
+    tokens = sum(seqs)
+    out = {
+        "metric": wl["metric"], "value": 1000.0 / ms, "unit": "forwards/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "tokens_per_s": tokens * 1000.0 / ms,
+        "workload": (f"Wan2.1-T2V-1.3B-architecture packed forward of 4 requests (grids "
+                     f"{', '.join('x'.join(map(str, gr)) for gr in grids)} = {tokens} tokens, cu_seqlens "
+                     f"[0, {', '.join(str(sum(seqs[:i + 1])) for i in range(4))}]), own timesteps U[0,1000) and "
+                     f"512-row texts (valid {valid}), {cfg.layers} blocks, one branch each"),
+        "tokens_per_step": tokens, "blocks": cfg.layers,
+        "model_tflops": total_flops / (ms * 1e-3) / 1e12,
+        "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "roofline": _roofline(f"flash_fwd_kernel<128> (self-attention, 4 segments, {tokens} tokens x "
+                              f"{cfg.heads} heads)", attn_flops, regions["attn_self"],
+                              algorithmic_bytes=4.0 * tokens * cfg.dim * 2),
+        "reference_a100_ms_per_step": None, "vs_reference_a100": None,
+        "_grids": grids,
+    }
+    if breakdown:
+        out["breakdown_ms_per_step"] = {k: v["total_ms"] / steps for k, v in regions.items()}
+    return out
+
+
+def run_sd35(steps, warmup, breakdown=False):
+    """SD3.5-Medium 1024^2 denoise step, CFG as a packed pair of joint segments
+    (4096 image + 333 text tokens each), 24 blocks, FlowMatch-Euler."""
+    import torch
+
     from ditserve_amd.sd35 import SD35_MEDIUM, SD35Transformer, forward_packed_sd35, step_flops
     from ditserve_amd.solver import FlowMatchEulerScheduler
 
@@ -232,7 +389,7 @@ def run_sd35(args):
     pooled_c = torch.randn((cfg.pooled_dim,), generator=g, device=dev)
     text_u, pooled_u = torch.zeros_like(text_c), torch.zeros_like(pooled_c)
     sched = FlowMatchEulerScheduler(shift=wl["shift"])
-    sched.set_timesteps(max(wl["steps"], args.warmup + args.steps))
+    sched.set_timesteps(max(wl["steps"], warmup + steps))
     n_img = (wl["latent"][1] // cfg.patch) * (wl["latent"][2] // cfg.patch)
     n_joint = n_img + wl["text_len"]
 
@@ -242,46 +399,140 @@ def run_sd35(args):
                                       [text_u.unsqueeze(0), text_c.unsqueeze(0)], [pooled_u, pooled_c])
         return sched.step(outs[1], t, lat, uncond=outs[0], guidance=7.0)[0]
 
-    for _ in range(args.warmup):
-        latent = step(latent)
-    torch.cuda.synchronize()
-    prof = EventProfiler(enabled=True, only=None if args.breakdown else {"attn_joint"})
-    model.profiler = prof
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        latent = step(latent)
-    end.record()
-    torch.cuda.synchronize()
-    model.profiler = EventProfiler(enabled=False)
+    latent, ms, regions = _timed(step, latent, steps, warmup, model, {"attn_joint"}, breakdown)
     if not bool(torch.isfinite(latent).all()):
-        raise RuntimeError("non-finite latent after the timed steps")
-    ms = start.elapsed_time(end) / args.steps
-    regions = prof.summary()
-    attn = regions["attn_joint"]
+        raise RuntimeError("sd35: non-finite latent after the timed steps")
     attn_flops = 4.0 * 2 * n_joint * n_joint * cfg.dim
-    attn_tflops = attn_flops / (attn["avg_ms"] * 1e-3) / 1e12
     total_flops = step_flops(cfg, [n_img, n_img], [wl["text_len"]] * 2)
     out = {
-        "metric": METRIC, "value": 1000.0 / ms, "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": (1000.0 / ms) / (1000.0 / wl["ref_ms"]), "dtype": "bf16",
-        "data": "synthetic: random-init weights N(0,0.02^2), latent/text/pooled N(0,1), uncond zeros",
-        "config": {"workload": f"SD3.5-Medium-architecture denoise step at 1024x1024 (latent 16x128x128), CFG pair "
-                               f"packed as 2 x ({n_img} image + {wl['text_len']} text) joint tokens, {cfg.layers} blocks "
-                               f"(13 with dual attention), FlowMatch-Euler shift {wl['shift']:g}",
-                   "tokens_per_step": 2 * n_joint, "blocks": cfg.layers},
-        "tokens_per_s": 2 * n_img * 1000.0 / ms,
+        "metric": wl["metric"], "value": 1000.0 / ms, "unit": "steps/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "tokens_per_s": 2 * n_img * 1000.0 / ms,
+        "workload": (f"SD3.5-Medium-architecture denoise step at 1024x1024 (latent 16x128x128), CFG pair packed "
+                     f"as 2 x ({n_img} image + {wl['text_len']} text) joint tokens, {cfg.layers} blocks (13 with "
+                     f"dual attention), FlowMatch-Euler shift {wl['shift']:g}"),
+        "tokens_per_step": 2 * n_joint, "blocks": cfg.layers,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-        "roofline": {"kernel": f"flash_fwd_kernel<64> (joint attention, 2 x {n_joint} tokens x {cfg.heads} heads)",
-                     "bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": attn_tflops / PEAK_BF16_TFLOPS, "traffic": None, "avg_launch_ms": attn["avg_ms"],
-                     "launches": attn["count"], "flops_per_launch": attn_flops},
-        "reference_a100_steps_per_s": 1000.0 / wl["ref_ms"],
+        "roofline": _roofline(f"flash_fwd_kernel<64> (joint attention, 2 x {n_joint} tokens x {cfg.heads} heads)",
+                              attn_flops, regions["attn_joint"], algorithmic_bytes=4.0 * 2 * n_joint * cfg.dim * 2),
+        "reference_a100_ms_per_step": wl["ref_ms"], "vs_reference_a100": wl["ref_ms"] / ms,
+        "_n_img": n_img, "_cfg": cfg,
     }
-    if args.breakdown:
-        out["breakdown_ms_per_step"] = {k: v["total_ms"] / args.steps for k, v in regions.items()}
+    if breakdown:
+        out["breakdown_ms_per_step"] = {k: v["total_ms"] / steps for k, v in regions.items()}
+    return out
+
+
+def run_wan_block(repeats=20):
+    """One Wan2.1 block on the 1x30x52 grid (1560 tokens, 77 valid text rows, t=500)."""
+    import torch
+
+    from ditserve_amd.wan import WanConfig, WanTransformer
+
+    cfg, dev = WanConfig(layers=1), "cuda"
+    model = WanTransformer.random(cfg, seed=0, device=dev)
+    g = torch.Generator().manual_seed(1)
+    lat = torch.randn((16, 1, 60, 104), generator=g).to(dev)
+    text = torch.randn((512, 4096), generator=g)
+    text[77:] = 0
+    packet = model.begin_packed_packet([lat], [500.0], [text.to(dev)])
+    h0 = packet["hidden"].clone()
+    for _ in range(3):
+        packet["hidden"] = h0.clone()
+        model.forward_block(packet, 0)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    inputs = [h0.clone() for _ in range(repeats)]
+    start.record()
+    for x in inputs:
+        packet["hidden"] = x
+        model.forward_block(packet, 0)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / repeats
+    return {"metric": "Wan2.1 block forward ms (1560 tokens)", "value": ms, "unit": "ms/block",
+            "higher_is_better": False, "steps": repeats, "warmup": 3, "tokens_per_s": 1560 * 1000.0 / ms,
+            "workload": "one Wan2.1-T2V-1.3B-architecture block, grid 1x30x52 (1560 tokens), 512 text rows "
+                        "(77 valid), t = 500, bf16"}
+
+
+def _public(d):
+    return {k: v for k, v in d.items() if not k.startswith("_")}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); this build "
+              "has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    threads = cpu_threads()
+    cpu = not args.no_cpu_baseline
+
+    def headline_for(name, steps, warmup, calibrate=False):
+        if name == "sd35_medium_1024":
+            return run_sd35(steps, warmup, args.breakdown)
+        if name == "wan21_packed_4req":
+            return run_wan_packed(steps, warmup, args.breakdown)
+        return run_wan_cfg(name, steps, warmup, args.breakdown, calibrate)
+
+    def cpu_for(name, res):
+        torch.set_num_threads(threads)
+        if name == "sd35_medium_1024":
+            return cpu_baseline_sd35(res["_cfg"], res["_n_img"], WORKLOADS[name]["text_len"], threads)
+        if name == "wan21_packed_4req":
+            from ditserve_amd.wan import WAN21_T2V_1_3B
+            return cpu_baseline_wan_packed(WAN21_T2V_1_3B, res["_grids"], threads)
+        label = "Wan2.1" if WORKLOADS[name]["arch"] == "wan21" else "Wan2.2-5B"
+        return cpu_baseline_wan_step(res["_cfg"], res["_grid"], threads, label)
+
+    head = headline_for(args.workload, args.steps, args.warmup, calibrate=args.workload == "wan21_480p")
+    out = {
+        "metric": head["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": head["vs_reference_a100"], "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0,0.02^2), latent/text N(0,1)",
+        "config": {"workload": head["workload"], "tokens_per_step": head["tokens_per_step"],
+                   "blocks": head["blocks"]},
+        "tokens_per_s": head["tokens_per_s"], "model_tflops": head["model_tflops"],
+        "model_mfma_frac": head["model_mfma_frac"], "roofline": head["roofline"],
+        "reference_a100_ms_per_step": head["reference_a100_ms_per_step"],
+    }
+    if "breakdown_ms_per_step" in head:
+        out["breakdown_ms_per_step"] = head["breakdown_ms_per_step"]
+    if cpu:
+        out["cpu_baseline"] = cpu_for(args.workload, head)
+    if not args.no_per_config:
+        per = {}
+        plan = [("wan21_480p", 3, 1), ("wan21_packed_4req", 5, 2), ("sd35_medium_1024", 10, 3),
+                ("wan22_ti2v_5b_704p", 3, 1)]
+        for name, steps, warmup in plan:
+            if name == args.workload:
+                res = dict(head)
+                if cpu:
+                    res["cpu_baseline"] = out["cpu_baseline"]
+            else:
+                _release()
+                res = headline_for(name, steps, warmup)
+                if cpu:
+                    res["cpu_baseline"] = cpu_for(name, res)
+            key = {"wan21_480p": "wan21_480p_cfg2", "wan21_packed_4req": "wan21_packed_4req",
+                   "sd35_medium_1024": "sd35_medium_1024_cfg2",
+                   "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2"}[name]
+            res.pop("breakdown_ms_per_step", None)
+            per[key] = _public(res)
+        _release()
+        blk = run_wan_block()
+        if cpu:
+            from ditserve_amd.wan import WAN21_T2V_1_3B
+            torch.set_num_threads(threads)
+            blk["cpu_baseline"] = cpu_baseline_wan_block(WAN21_T2V_1_3B, threads)
+            blk["gpu_vs_cpu"] = blk["cpu_baseline"]["value"] / blk["value"]
+        per["wan21_block_1560tok"] = blk
+        out["per_config"] = per
     print(json.dumps(out), flush=True)
 
 

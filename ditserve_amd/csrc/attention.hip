@@ -46,22 +46,10 @@
 
 namespace {
 
-constexpr int BN = 64;   // keys per iteration
-#ifndef ATTN_NW
-#define ATTN_NW 8        // waves per workgroup
-#endif
-#ifndef ATTN_QB
-#define ATTN_QB 1        // 32-query blocks per wave
-#endif
-#ifndef ATTN_SPLIT
-#define ATTN_SPLIT 1     // softmax pairs spread over both MFMA phases of a tile (0: compiler order)
-#endif
-#ifndef ATTN_KEARLY
-#define ATTN_KEARLY 1    // K fragments of chunk c+1 read right after chunk c's first MFMA
-#endif
-#ifndef ATTN_VAHEAD
-#define ATTN_VAHEAD 2    // Vt fragments in flight ahead of the PV MFMAs
-#endif
+constexpr int BN = 64;        // keys per iteration
+constexpr int kWaves = 8;     // waves per workgroup: two per SIMD
+constexpr int kQBlocks = 1;   // 32-query blocks per wave
+constexpr int kVAhead = 2;    // Vt fragments in flight ahead of the PV MFMAs
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max is raised
 constexpr float kRescaleSum = 256.0f;  // 2^kLazy: a lane's row sum above it triggers a rescale
 
@@ -225,7 +213,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int v = 0; v < 16; ++v) o[qb][d][v] = 0.f;
-  static_assert(!PRE || (ATTN_SPLIT && HD == 64), "pre-scaled Q: split loop, head_dim 64");
+  static_assert(!PRE || HD == 64, "pre-scaled Q: head_dim 64");
   constexpr float kOne = 1.0f;
   const float sc = PRE ? kOne : scale_log2;  // S -> log2 units
   float m_run[QB], l_run[QB];
@@ -472,7 +460,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     dma_wait();
     __syncthreads();
   }
-#if ATTN_SPLIT
   // Split interleave: the 16 score pairs of a tile are spread evenly over both
   // MFMA phases of the wave.  Per tile kt:
   //   phase 1: S(kt+1) = K(kt+1) Q^T   ||  P(kt) keys 32..63
@@ -574,14 +561,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
         for (int kk = 0; kk < 2; ++kk) {
           const int slot = c * 2 + kk;
           __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
-#if ATTN_KEARLY
           if (kk == 0 && c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#endif
           valu_group(slot_ops(slot, SLOTS, 8 * QB));
         }
-#if !ATTN_KEARLY
-        if (c + 1 < NC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#endif
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -610,7 +592,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
     {
       constexpr int SLOTS = 4 * DT;
       float ph2[8 * QB][2];
-      constexpr int VA = ATTN_VAHEAD;  // Vt fragments in flight
+      constexpr int VA = kVAhead;  // Vt fragments in flight
       bf16x8_t vb[VA + 1];
 #pragma unroll
       for (int t = 0; t < VA; ++t) vb[t] = v_frag(vcur, t / DT, t % DT);
@@ -662,28 +644,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       last(sa);
     }
   }
-#else
-  // Compiler-ordered loop: P(kt), the (rare) rescale, then S(kt+1) and PV(kt);
-  // only the other wave of the SIMD overlaps softmax with MFMAs.
-  for (int kt = 0; kt + 1 < nkt; ++kt) {  // every tile but the last: all 64 keys valid
-    const int kcur = kt % KST, knxt = (kt + 1) % KST, vcur = kt & 1;
-    if (kt + 2 < nkt) issue_k(kt + 2, (kt + 2) % KST);
-    issue_v(kt + 1, vcur ^ 1);
-    uint32_t pf[QB][2][2][4];
-    float rs[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rs[qb] = softmax_p(s_next[qb], pf[qb], m_run[qb], BN);
-    pin(pf);
-    if (needs_rescale(rs)) rescale_tile(kcur, pf, rs, BN);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) l_run[qb] += rs[qb];
-    compute_s(knxt, s_next);
-    pv(vcur, pf);
-    dma_wait();
-    __syncthreads();
-  }
-  if (nkt > 0) last(s_next);
-#endif
 
   // ---- normalise and store
 #pragma unroll
@@ -846,13 +806,13 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
   };
   int rc;
   if (joint)
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true, true>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, true>, kWaves * kQBlocks * 32, kWaves * 64);
   else if (pre)
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, true, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, false>, kWaves * kQBlocks * 32, kWaves * 64);
   else if (head_dim == 128)
-    rc = run(flash_fwd_kernel<128, ATTN_NW, ATTN_QB, false, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<128, kWaves, kQBlocks, false, false>, kWaves * kQBlocks * 32, kWaves * 64);
   else
-    rc = run(flash_fwd_kernel<64, ATTN_NW, ATTN_QB, false, false>, ATTN_NW * ATTN_QB * 32, ATTN_NW * 64);
+    rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, false, false>, kWaves * kQBlocks * 32, kWaves * 64);
   if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
 }

@@ -394,22 +394,20 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const fl
   return ditk_check_launch("ditk_gemm");
 }
 
-// Small tiles when the large ones would number fewer than GEMM_SMALL_BELOW: the
+// Small tiles when the large ones would number fewer than kSmallBelow: the
 // choice cannot change a result, only how many CUs take part.  Measured per CU,
 // a small workgroup alone on a CU runs at about half a large one's rate and two
 // sharing one at about a quarter each, so small tiles (8 per large tile) win
 // while they fit about two per CU: 666-row text GEMMs 1.3-3x faster (54-72
 // large tiles), 8192 x 1536 1.25-1.5x slower (192 large tiles).
-#ifndef GEMM_SMALL_BELOW
-#define GEMM_SMALL_BELOW 128
-#endif
+constexpr int64_t kSmallBelow = 128;
 template <int EPI, int BK>
 int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
            int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
            int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream) {
   using L = Tile<TILE_LARGE>;
   const int64_t large_tiles = (int64_t)((M + L::GBM - 1) / L::GBM) * ((N + L::GBN - 1) / L::GBN);
-  if (large_tiles < GEMM_SMALL_BELOW)
+  if (large_tiles < kSmallBelow)
     return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }

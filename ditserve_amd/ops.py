@@ -100,6 +100,14 @@ class Segments:
     def lengths(self):
         return [b - a for a, b in zip(self.cu, self.cu[1:])]
 
+    def device_tensors(self):
+        return (self.dev,)
+
+    def record_stream(self, stream):
+        """Mark the device table as in use by ``stream`` (for packets consumed on a
+        side stream, as the reference's interleaved executor does)."""
+        self.dev.record_stream(stream)
+
 
 # ---------------------------------------------------------------------------
 # normalisation
@@ -181,6 +189,13 @@ class Rope:
 
     def __len__(self):
         return 2
+
+    def device_tensors(self):
+        return (self.cos, self.sin, self.grids, *self.segments.device_tensors())
+
+    def record_stream(self, stream):
+        for t in self.device_tensors():
+            t.record_stream(stream)
 
 
 def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None):

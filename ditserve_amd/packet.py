@@ -30,8 +30,11 @@ def digest(t):
 
 
 def engine_info():
+    """Engine name and revision, as the reference's engine_info() reports them
+    (workers/ditserve/models/xdit/__init__.py:7-8); a payload imports only into an
+    engine of the same revision."""
     from . import _lib
-    return {"engine": "ditk", "revision": f"ditk-{int(_lib.load().ditk_version())}"}
+    return {"name": "ditk", "revision": f"ditk-{int(_lib.load().ditk_version())}"}
 
 
 def export_packet(packet, engine=None):

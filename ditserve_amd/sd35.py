@@ -184,7 +184,8 @@ class SD35Transformer:
         self.ctx = (w("context_embedder.weight"), f("context_embedder.bias"))
         self.norm_out = (w("norm_out.linear.weight"), f("norm_out.linear.bias"))
         self.proj_out = (w("proj_out.weight"), f("proj_out.bias"))
-        self._q_pre = cfg.head_dim == 64
+        if cfg.head_dim != 64:
+            raise ValueError("the SD3.5 joint attention kernels take head_dim 64 (SD3.5 uses 64)")
         self._q_mult = ops.LOG2E / math.sqrt(cfg.head_dim)
         self.blocks = []
         for i in range(cfg.layers):
@@ -216,13 +217,12 @@ class SD35Transformer:
                                torch.cat([f(f"{a2}.to_q.bias"), f(f"{a2}.to_k.bias"), f(f"{a2}.to_v.bias")]))
                 blk["nq2"], blk["nk2"] = per_head(f"{a2}.norm_q.weight"), per_head(f"{a2}.norm_k.weight")
                 blk["out2"] = (w(f"{a2}.to_out.0.weight"), f(f"{a2}.to_out.0.bias"))
-            # head_dim 64: the q-side RMSNorm weights carry softmax_scale * log2(e),
-            # so the normed q leaves the norm kernel pre-scaled (still one bf16
-            # rounding) and attention skips its per-score scaling
-            if self._q_pre:
-                for key in ("nq", "nqt", "nq2"):
-                    if key in blk:
-                        blk[key + "_pre"] = blk[key] * self._q_mult
+            # the q-side RMSNorm weights carry softmax_scale * log2(e), so the normed
+            # q leaves the norm kernel pre-scaled (still one bf16 rounding) and
+            # attention skips its per-score scaling
+            for key in ("nq", "nqt", "nq2"):
+                if key in blk:
+                    blk[key + "_pre"] = blk[key] * self._q_mult
             self.blocks.append(blk)
         # Every AdaLN modulation projection (norm1, norm1_context of each block,
         # norm_out) reads the same conditioning rows silu(temb), so all of them
@@ -259,11 +259,11 @@ class SD35Transformer:
     # ------------------------------------------------------------------ pieces
     def _attention(self, qkv, seg, wq, wk):
         """Per-head QK RMSNorm (in place on the qkv buffer) + varlen flash over seg
-        (wq already carries the pre-scale when self._q_pre)."""
+        (wq carries the softmax pre-scale)."""
         D, H, Dh = self.cfg.dim, self.cfg.heads, self.cfg.head_dim
         q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
         ops.qk_norm_rope_(q, k, wq, wk, Dh, self.cfg.eps, per_head=True)
-        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh, q_prescaled=self._q_pre)
+        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh, q_prescaled=True)
 
     def _block(self, i, h, c, mod, seg_img, seg_txt, seg_joint):
         cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
@@ -280,38 +280,25 @@ class SD35Transformer:
         with prof.region("gemm_qkv"):
             qkv_i = ops.linear(nh, *blk["qkv"])
             qkv_t = ops.linear(nc, *blk["qkv_t"])
-        pre = "_pre" if self._q_pre else ""
         with prof.region("joint_prep"):
             D3 = 3 * D
-            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq" + pre], blk["nk"], cfg.head_dim, eps,
+            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq_pre"], blk["nk"], cfg.head_dim, eps,
                               per_head=True)
-            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt" + pre], blk["nkt"], cfg.head_dim, eps,
+            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt_pre"], blk["nkt"], cfg.head_dim, eps,
                               per_head=True)
-            if self._q_pre:  # image and text rows read in place: no gather / scatter copies
-                vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
-                                           seg_img, seg_txt, seg_joint)
-            else:
-                joint = ops.joint_gather(qkv_i, qkv_t, seg_img, seg_txt)  # [T_joint, 3D]
-                vt = ops.transpose_v(joint[:, 2 * D:D3], cfg.heads, cfg.head_dim, seg_joint)
+            # image and text rows are read in place: no gather / scatter copies
+            vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
+                                       seg_img, seg_txt, seg_joint)
         with prof.region("attn_joint"):
-            if self._q_pre:
-                a_img, a_txt = ops.joint_attention_q_prescaled(
-                    qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D], vt, seg_img, seg_txt,
-                    seg_joint, cfg.heads, cfg.head_dim)
-            else:
-                a = ops.flash_attn_varlen(joint[:, :D], joint[:, D:2 * D], None, seg_joint, seg_joint,
-                                          cfg.heads, cfg.head_dim, vt=vt)
-        if not self._q_pre:
-            with prof.region("joint_scatter"):
-                a_img = torch.empty((seg_img.total, D), dtype=_BF16, device=h.device)
-                a_txt = torch.empty((seg_txt.total, D), dtype=_BF16, device=h.device)
-                ops.joint_scatter(a, a_img, a_txt, seg_img, seg_txt)
+            a_img, a_txt = ops.joint_attention_q_prescaled(
+                qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D], vt, seg_img, seg_txt,
+                seg_joint, cfg.heads, cfg.head_dim)
         with prof.region("gemm_out"):
             h = ops.linear(a_img, *blk["out"], "gate_res", residual=h, gate=emb[:, 2 * D:3 * D], segments=seg_img)
         if blk["dual"]:
             with prof.region("attn_dual"):
                 qkv2 = ops.linear(nh2, *blk["qkv2"])
-                a2 = self._attention(qkv2, seg_img, blk["nq2_pre" if self._q_pre else "nq2"], blk["nk2"])
+                a2 = self._attention(qkv2, seg_img, blk["nq2_pre"], blk["nk2"])
                 ops.linear(a2, *blk["out2"], "gate_res", residual=h, gate=emb[:, 8 * D:9 * D], segments=seg_img, out=h)
         with prof.region("ffn"):
             n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)
@@ -375,6 +362,7 @@ class SD35Transformer:
         meta = {
             "sequence_packed": True,
             "attention_backend": "ditk_flash_varlen",
+            "attention_provider": "ditk",
             "packed_segments": n,
             "cu_seqlens_img": lay["cu_img"],
             "cu_seqlens_txt": lay["cu_txt"],
@@ -429,3 +417,95 @@ def step_flops(cfg, img_counts, txt_counts):
             if dual:
                 total += 2 * n * D * 3 * D + 4 * n * n * D + 2 * n * D * D
     return total
+
+
+def step_members_once(model, states, *, force_packing=False):
+    """One denoising step of every state (mixed timesteps, resolutions, prompt
+    lengths and CFG), as workers/ditserve/models/sd35.py:895-1020 does it: a CFG
+    state contributes its unconditional then its conditional segment, and each
+    state's scheduler steps on the CFG-combined output.  Every batch runs as one
+    packed forward on the ditk kernels (a homogeneous batch is the packed batch of
+    equal segments); the returned meta says which form the reference would take.
+
+    A state is a dict with ``latents`` [1, C, h, w] fp32, ``timesteps``, ``step``,
+    ``spec`` (``height``, ``width``, ``guidance_scale``), ``embeds``
+    (``prompt_embeds`` [1, L, text_dim], ``pooled_prompt_embeds`` [1, pooled_dim]
+    and their ``negative_`` forms for CFG) and ``scheduler`` (a
+    FlowMatchEulerScheduler)."""
+    resolutions = [(int(st["spec"]["height"]), int(st["spec"]["width"])) for st in states]
+    cfg_flags = [float(st["spec"]["guidance_scale"]) > 1.0 for st in states]
+    txt_lens = [int(st["embeds"]["prompt_embeds"].shape[1]) for st in states]
+    use_packing = bool(force_packing or len(set(resolutions)) > 1 or len(set(cfg_flags)) > 1
+                       or len(set(txt_lens)) > 1)
+    lats, ts, encs, pooled, seg_map = [], [], [], [], []
+    for idx, st in enumerate(states):
+        t = st["timesteps"][int(st["step"])]
+        emb = st["embeds"]
+        s_uncond = None
+        if cfg_flags[idx]:
+            s_uncond = len(lats)
+            lats.append(st["latents"])
+            ts.append(t)
+            encs.append(emb["negative_prompt_embeds"])
+            pooled.append(emb["negative_pooled_prompt_embeds"])
+        seg_map.append((idx, s_uncond, len(lats)))
+        lats.append(st["latents"])
+        ts.append(t)
+        encs.append(emb["prompt_embeds"])
+        pooled.append(emb["pooled_prompt_embeds"])
+    outs, meta = forward_packed_sd35(torch, model, lats, ts, encs, pooled)
+    for idx, s_uncond, s_cond in seg_map:
+        st = states[idx]
+        t = st["timesteps"][int(st["step"])]
+        guidance = float(st["spec"]["guidance_scale"])
+        uncond = outs[s_uncond] if s_uncond is not None else None
+        st["latents"] = st["scheduler"].step(outs[s_cond], t, st["latents"], return_dict=False, uncond=uncond,
+                                             guidance=guidance if uncond is not None else 1.0)[0]
+        st["step"] = int(st["step"]) + 1
+    if use_packing:
+        return meta
+    return {"sequence_packed": False, "vector_timesteps": [float(st["timesteps"][int(st["step"]) - 1])
+                                                           for st in states], "batch_size": len(states)}
+
+
+def advance_batch(model, states, state_ids, steps=1, *, sequence_packing=False, vae_scale_factor=8):
+    """Advance 1..8 states by ``steps`` denoising steps in shared packed forwards and
+    report the result in the shape of the reference's batched advance
+    (workers/ditserve/models/sd35.py:1025-1164): per-state progress, the wall time
+    (``model_ms``), the batch's packing summary, the last step's meta."""
+    import time
+
+    from .executor import memory, progress
+    from .packing import packing_stats
+
+    if not isinstance(state_ids, list) or not 1 <= len(state_ids) <= 8 or len(set(state_ids)) != len(state_ids):
+        raise ValueError("advance_batch requires 1 to 8 distinct state_ids")
+    if len(states) != len(state_ids):
+        raise ValueError("one state per state id")
+    if type(steps) is not int or steps < 1:
+        raise ValueError("steps must be a positive integer")
+    for sid, st in zip(state_ids, states):
+        if int(st.get("step", 0)) >= int(st.get("steps", st["spec"]["steps"])):
+            raise ValueError(f"state {sid} has already completed")
+    torch.cuda.synchronize()
+    started = time.perf_counter()
+    step_meta = {}
+    for st in states:
+        st["steps"] = int(st.get("steps", st["spec"]["steps"]))
+        st["step"] = int(st.get("step", 0))
+    for _ in range(steps):
+        active = [st for st in states if int(st["step"]) < int(st["steps"])]
+        if not active:
+            break
+        step_meta = step_members_once(model, active, force_packing=sequence_packing)
+    torch.cuda.synchronize()
+    elapsed_ms = (time.perf_counter() - started) * 1000.0
+    pack = packing_stats([int(st["spec"]["height"]) for st in states], [int(st["spec"]["width"]) for st in states],
+                         vae_scale_factor=vae_scale_factor, patch_size=model.cfg.patch)
+    results = []
+    for sid, st in zip(state_ids, states):
+        st["paused"] = int(st["step"]) < int(st["steps"])
+        results.append(dict(state_id=sid, progress=progress(int(st["step"]), int(st["steps"])), paused=st["paused"]))
+    return dict(results=results, batch_size=len(state_ids), quantum="continuous_batch", model_ms=round(elapsed_ms, 3),
+                attention="ditk", bubble_free=False, sequence_packing=bool(step_meta.get("sequence_packed", False)),
+                packing=pack, step_meta=step_meta, memory_after=memory())

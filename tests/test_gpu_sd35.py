@@ -95,3 +95,54 @@ def test_sd35_config3_packed_cfg_batch_bitwise():
                                            [pools[i]])
         assert torch.isfinite(solo[0]).all()
         assert torch.equal(outs[i], solo[0]), f"segment {i} differs"
+
+
+REFERENCE_BATCH = {"results", "batch_size", "quantum", "model_ms", "attention", "bubble_free", "sequence_packing",
+                   "packing", "step_meta", "memory_after"}
+REFERENCE_META = {"sequence_packed", "attention_backend", "attention_provider", "packed_segments", "cu_seqlens_img",
+                  "cu_seqlens_txt", "packed_image_tokens", "padded_image_tokens", "padding_saved_tokens"}
+
+
+def _state(seed, res, steps, guidance):
+    from ditserve_amd.solver import FlowMatchEulerScheduler
+    lat, txt, pooled = _inputs(seed, res)
+    sched = FlowMatchEulerScheduler(shift=3.0)
+    sched.set_timesteps(steps)
+    emb = dict(prompt_embeds=txt.unsqueeze(0).to(DEV), pooled_prompt_embeds=pooled.unsqueeze(0).to(DEV),
+               negative_prompt_embeds=torch.zeros(1, 333, 4096, device=DEV),
+               negative_pooled_prompt_embeds=torch.zeros(1, 2048, device=DEV))
+    return dict(latents=lat.unsqueeze(0).to(DEV), timesteps=sched.timesteps, step=0,
+                spec=dict(height=res, width=res, guidance_scale=guidance, steps=steps), embeds=emb, scheduler=sched)
+
+
+def test_sd35_advance_batch_result_and_packing_invariance():
+    """workers/ditserve/models/sd35.py:1025-1164: the batched advance of a mixed batch
+    (two resolutions, one state without CFG) packs every segment, reports the
+    reference's fields, and leaves each state where its solo advance leaves it."""
+    sd35 = _sd()
+    cfg = sd35.SD35Config(layers=3, dual_layers=(0,))
+    model = sd35.SD35Transformer.random(cfg, seed=4, device=DEV)
+    specs = [(60, 256, 2, 5.0), (61, 128, 2, 1.0)]
+    states = [_state(*s) for s in specs]
+    res = sd35.advance_batch(model, states, ["a", "b"], steps=1)
+    assert set(res) == REFERENCE_BATCH and res["sequence_packing"] is True
+    assert REFERENCE_META <= set(res["step_meta"]) and res["step_meta"]["packed_segments"] == 3
+    assert res["packing"]["image_token_counts"] == [256, 64] and res["packing"]["heterogeneous_resolutions"]
+    assert [r["progress"]["step"] for r in res["results"]] == [1, 1] and all(r["paused"] for r in res["results"])
+    for s, st in zip(specs, states):
+        solo = _state(*s)
+        sd35.advance_batch(model, [solo], ["x"], steps=1)
+        assert torch.equal(solo["latents"], st["latents"])
+    res = sd35.advance_batch(model, states, ["a", "b"], steps=3)
+    assert all(r["progress"]["done"] and not r["paused"] for r in res["results"])
+    # homogeneous batch: the reference's dense form is reported (same packed kernels run)
+    homo = [_state(70, 128, 1, 5.0), _state(71, 128, 1, 5.0)]
+    res = sd35.advance_batch(model, homo, ["c", "d"])
+    assert res["sequence_packing"] is False and res["step_meta"]["batch_size"] == 2
+    forced = [_state(70, 128, 1, 5.0), _state(71, 128, 1, 5.0)]
+    res2 = sd35.advance_batch(model, forced, ["c", "d"], sequence_packing=True)
+    assert res2["sequence_packing"] is True
+    for a, b in zip(homo, forced):
+        assert torch.equal(a["latents"], b["latents"])
+    with pytest.raises(ValueError):
+        sd35.advance_batch(model, homo, ["c", "d"])  # both finished

@@ -42,6 +42,8 @@ SIGNATURES = {
     "ditk_joint_copy": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "ditk_silu": (c_int, [_P, _P, c_int64, _P]),
     "ditk_solver_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P]),
+    "ditk_flash_attn_varlen_noalloc": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64,
+                                               _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P]),
 }
 
 _lib = None

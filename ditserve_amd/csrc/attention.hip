@@ -42,6 +42,8 @@
 // of the "b" operand (text tokens) — for Q, K and O alike, so SD3.5's image and
 // text projections feed joint attention, and take its output, without a gather
 // or scatter copy.  Results are bitwise those of the gathered layout.
+#include <mutex>
+
 #include "ditk_common.h"
 
 namespace {
@@ -847,4 +849,63 @@ DITK_EXPORT int ditk_joint_attn_q_prescaled(const void* q_a, const void* q_b, in
   DITK_REQUIRE(cu_a && cu_b, "ditk_joint_attn_q_prescaled: null segment table");
   return flash_launch(q_a, ldq, k_a, ldk, vt, vt_ld, o_a, ldo, nullptr, 0, cu_joint, cu_joint, nseg, T_joint, heads,
                       head_dim, 1.0f, true, stream, q_b, k_b, o_b, cu_a, cu_b);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free attention: the transposed-V staging lives in a file-scope
+// device array instead of a caller- or library-allocated buffer.  Each GPU holds
+// its own copy of the array (kScratchBytes) until the process ends; its device
+// address is looked up once per device, with that device current, and only that
+// address is handed to kernels.  Every call on a GPU shares the array, so calls
+// that overlap on one GPU (different streams) race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = size_t(64) << 20;  // DITK_NOALLOC_SCRATCH_BYTES of include/ditk.h
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// device address of `scratch` on the current device (nullptr + message on failure)
+void* scratch_ptr() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    ditk_set_error("ditk_flash_attn_varlen_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      ditk_set_error("ditk_flash_attn_varlen_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+DITK_EXPORT int ditk_flash_attn_varlen_noalloc(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                               const void* v, int64_t ldv, void* o, int64_t ldo, float* lse,
+                                               int64_t lse_ld, const int32_t* cu_q, const int32_t* cu_k, int nseg,
+                                               int Tq, int Tk, int heads, int head_dim, float softmax_scale,
+                                               hipStream_t stream) {
+  DITK_REQUIRE(v != nullptr, "ditk_flash_attn_varlen_noalloc: null tensor");
+  DITK_REQUIRE(Tk >= 0 && nseg > 0 && heads > 0 && (head_dim == 64 || head_dim == 128),
+               "ditk_flash_attn_varlen_noalloc: bad sizes");
+  const int64_t cols = ditk_vt_columns(Tk, nseg);
+  const size_t need = (size_t)heads * (size_t)head_dim * (size_t)cols * sizeof(bf16_t);
+  DITK_REQUIRE(need <= kScratchBytes,
+               "ditk_flash_attn_varlen_noalloc: transposed V needs %zu bytes (%d heads x %d x %lld columns), "
+               "more than the %zu-byte scratch; use ditk_transpose_v + ditk_flash_attn_varlen with a caller buffer",
+               need, heads, head_dim, (long long)cols, kScratchBytes);
+  void* vt = scratch_ptr();
+  if (vt == nullptr) return 3;
+  int rc = ditk_transpose_v(v, ldv, vt, cols, Tk, heads, head_dim, cu_k, nseg, stream);
+  if (rc) return rc;
+  return ditk_flash_attn_varlen(q, ldq, k, ldk, vt, cols, o, ldo, lse, lse_ld, cu_q, cu_k, nseg, Tq, heads,
+                                head_dim, softmax_scale, stream);
 }

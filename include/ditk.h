@@ -200,6 +200,27 @@ int ditk_solver_step(const float* x, const float* cond, const float* uncond, con
                      const float* m_prev, const float* m_prev2, float* x_next, float* x_corr, float* m_out,
                      int64_t n, const float* coef, ditk_stream_t stream);
 
+/* Size of the per-GPU scratch array behind ditk_flash_attn_varlen_noalloc (64 MiB). */
+#define DITK_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * ditk_flash_attn_varlen that allocates nothing: V is taken row-major
+ * ([Tk, ldv], head h at columns h*head_dim, as ditk_transpose_v takes it) and
+ * transposed into a file-scope device array of DITK_NOALLOC_SCRATCH_BYTES that
+ * each GPU holds until the process ends, then attended exactly as by
+ * ditk_transpose_v + ditk_flash_attn_varlen (bitwise the same outputs and lse).
+ * Calls needing more than the scratch (heads * head_dim * ditk_vt_columns(Tk,
+ * nseg) * 2 bytes) are rejected before any launch.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (on different streams) race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int ditk_flash_attn_varlen_noalloc(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                   void* o, int64_t ldo, float* lse, int64_t lse_ld, const int32_t* cu_q,
+                                   const int32_t* cu_k, int nseg, int Tq, int Tk, int heads, int head_dim,
+                                   float softmax_scale, ditk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@
 #include <mutex>
 
 #include "ditk_common.h"
+#include "attn_d128_clobbers.h"
 
 namespace {
 
@@ -674,6 +675,106 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   }
 }
 
+// head_dim 128, 64 queries per wave (two 32-query blocks), one wave per SIMD:
+// four waves and 256 queries per workgroup.  The C++ side locates the work item
+// and computes per-lane addresses; the body is generated assembly
+// (gen_attn_d128.py -> attn_d128_body.inc) with its registers placed by hand:
+// O^T and Q in AGPRs, S^T and P in VGPRs, so that the whole working set (about
+// 460 registers per lane) stays in registers.  Same arithmetic, same order of
+// every sum and the same lazy-rescale rule as flash_fwd_kernel, per score.
+__global__ __launch_bounds__(256, 1) void flash_fwd_d128(
+    const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
+    const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
+    float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
+    const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
+  constexpr int HD = 128, NW = 4, BM = 256;
+  __shared__ u32x4_t Ks[2][BN * HD / 8];
+  __shared__ u32x4_t Vs[2][HD * 8];
+  const int nb = gridDim.x;
+  const int b = blockIdx.x;
+  const int logical = (b & 7) * (nb >> 3) + (b >> 3);
+  const int head = logical / tiles_bound;
+  int t = logical % tiles_bound;
+  if (head >= heads) return;
+  const int seg = locate_tile(cu_q, nseg, BM, t);
+  if (seg < 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int q_end = cu_q[seg + 1];
+  const int qrow0 = cu_q[seg] + t * BM + wave * 64 + l32;
+  const int qrow1 = qrow0 + 32;
+  const int k_beg = cu_k[seg], k_len = cu_k[seg + 1] - k_beg;
+  if (k_len <= 0) {  // no keys: zero output rows, lse -inf (nothing to attend)
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qrow = qb ? qrow1 : qrow0;
+      if (qrow < q_end) {
+        for (int d = hh * 64; d < hh * 64 + 64; ++d) O[(int64_t)qrow * ldo + (int64_t)head * HD + d] = 0;
+        if (lse != nullptr && hh == 0) lse[(int64_t)head * lse_ld + qrow] = -INFINITY;
+      }
+    }
+    return;
+  }
+  const int nkt = (k_len + BN - 1) / BN;
+  const int valid_last = k_len - (nkt - 1) * BN;
+  const int pk = padded_key_start(cu_k, seg);
+  // Q rows past the segment end read its last row (their outputs are not stored)
+  const uint64_t qbase = (uint64_t)(uintptr_t)(Q + (int64_t)head * HD);
+  const uint32_t qoff0 = (uint32_t)((int64_t)min(qrow0, q_end - 1) * ldq * 2 + hh * 16);
+  const uint32_t qoff1 = (uint32_t)((int64_t)min(qrow1, q_end - 1) * ldq * 2 + hh * 16);
+  const uint64_t kdma = (uint64_t)(uintptr_t)(Kp + (int64_t)head * HD + (int64_t)k_beg * ldk);
+  const uint64_t vdma = (uint64_t)(uintptr_t)(Vt + (int64_t)head * vt_hs + pk);
+  const uint32_t ktile = (uint32_t)(BN * ldk * 2);
+  const uint32_t ldkb = (uint32_t)(ldk * 2);
+  // LDS read bases (bytes within a stage), as flash_fwd_kernel's kbase / vbase
+  const int kr = kperm(l32), kg = (kr >> 1) & 7, vg = (l32 >> 1) & 7;
+  uint32_t kb[4], vb[4], krow[4], kcolb[4], voff[4];
+  const int lrow = lane >> 3;
+  const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;
+  const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kb[i] = (uint32_t)(kr * 8 + ((i * 2 + hh) ^ kg)) * 16;
+    vb[i] = (uint32_t)(l32 * 8 + ((i * 2 + hh) ^ vg)) * 16;
+    const int g = i * NW + wave_u;
+    const int grp = g / (BN / 8), r8 = g % (BN / 8);
+    krow[i] = (uint32_t)(r8 * 8 + lrow);
+    kcolb[i] = (uint32_t)(grp * 64 + ((r8 & 1) ? lsw1 : lsw0)) * 2;
+    voff[i] = (uint32_t)((int64_t)(g * 8 + lrow) * vt_ld + ((g & 1) ? lsw1 : lsw0)) * 2;
+  }
+  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Ks[0][0];
+  const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Vs[0][0];
+  const uint32_t wave1k = (uint32_t)wave_u * 1024u;
+  const uint32_t xaddr = (uint32_t)((lane ^ 32) * 4);
+  const uint32_t hh8 = (uint32_t)(hh * 8);
+  const uint32_t lanev = (uint32_t)lane;
+  const uint64_t obase = (uint64_t)(uintptr_t)(O + (int64_t)head * HD);
+  const uint32_t ldob = (uint32_t)(ldo * 2);
+  const uint64_t lsebase = (uint64_t)(uintptr_t)(lse != nullptr ? lse + (int64_t)head * lse_ld : lse);
+  const uint32_t has_lse = lse != nullptr;
+  // scalar operands: wave-uniform values, made SGPR-resident explicitly
+  auto su = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+  auto su64 = [&](uint64_t x) { return ((uint64_t)su((uint32_t)(x >> 32)) << 32) | su((uint32_t)x); };
+  const float sc = __builtin_bit_cast(float, su(__builtin_bit_cast(uint32_t, scale_log2)));
+  asm volatile(
+#include "attn_d128_body.inc"
+      :
+      : [qbase] "s"(su64(qbase)), [qoff0] "v"(qoff0), [qoff1] "v"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),
+        [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),
+        [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),
+        [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [ldkb] "s"(su(ldkb)),
+        [wave1k] "s"(su(wave1k)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)),
+        [obase_lo] "s"(su((uint32_t)obase)), [obase_hi] "s"(su((uint32_t)(obase >> 32))),
+        [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)), [kbase0] "v"(kb[0]), [kbase1] "v"(kb[1]),
+        [kbase2] "v"(kb[2]), [kbase3] "v"(kb[3]), [vbase0] "v"(vb[0]), [vbase1] "v"(vb[1]), [vbase2] "v"(vb[2]),
+        [vbase3] "v"(vb[3]), [krow0] "v"(krow[0]), [krow1] "v"(krow[1]), [krow2] "v"(krow[2]),
+        [krow3] "v"(krow[3]), [kcolb0] "v"(kcolb[0]), [kcolb1] "v"(kcolb[1]), [kcolb2] "v"(kcolb[2]),
+        [kcolb3] "v"(kcolb[3]), [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]),
+        [voff3] "v"(voff[3]), [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0),
+        [qrow1] "v"(qrow1)
+      : DITK_D128_CLOBBERS "vcc", "scc", "memory");
+}
+
 // V [Tk, ldv] (head h at columns h*HD..) -> Vt [heads][HD][vt_ld], per-segment
 // 64-aligned columns, zero padding.  One workgroup per (64-key tile, head).
 // With cu_a != nullptr the segment's rows come from V (rows cu_a[m] + j) and Vb
@@ -811,8 +912,19 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, true>, kWaves * kQBlocks * 32, kWaves * 64);
   else if (pre)
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, false>, kWaves * kQBlocks * 32, kWaves * 64);
-  else if (head_dim == 128)
-    rc = run(flash_fwd_kernel<128, kWaves, kQBlocks, false, false>, kWaves * kQBlocks * 32, kWaves * 64);
+  else if (head_dim == 128) {
+    // one wave per SIMD, 64 queries per wave: generated-assembly body
+    DITK_REQUIRE((int64_t)Tq * ldq * 2 < (1ll << 32) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
+                 "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
+    const int tiles_bound = (Tq + 255) / 256 + nseg;
+    int64_t nblocks = (int64_t)tiles_bound * heads;
+    nblocks = (nblocks + 7) / 8 * 8;
+    DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
+    flash_fwd_d128<<<(unsigned)nblocks, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk,
+                                                        (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld,
+                                                        cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+    rc = 0;
+  }
   else
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, false, false>, kWaves * kQBlocks * 32, kWaves * 64);
   if (rc) return rc;

@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
     const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
   constexpr int HD = 128, NW = 4, BM = 256;
   __shared__ u32x4_t Ks[2][BN * HD / 8];
-  __shared__ u32x4_t Vs[2][HD * 8];
+  __shared__ u32x4_t Vs[3][HD * 8];
   const int nb = gridDim.x;
   const int b = blockIdx.x;
   const int logical = (b & 7) * (nb >> 3) + (b >> 3);

@@ -65,9 +65,12 @@ S_CMP = 74       # s[74:75] compare mask
 S_EXEC = 76      # s[76:77] saved exec
 S_VALID = 78     # s78 valid keys of the last tile
 S_M0 = 79        # s79 M0 staging
-SGPRS = list(range(60, 80))
+S_V3 = 80        # s80 the third Vt stage (read two tiles from now)
+SGPRS = list(range(60, 81))
 
 BN, HD = 64, 128
+# schedule options (the defaults are the shipped schedule)
+OPTS = {"p2wait": 2, "dma_slots": True, "barrier_slot": 32}
 KSTAGE_BYTES = BN * HD * 2     # 16 KiB
 VSTAGE_BYTES = HD * BN * 2     # 16 KiB
 
@@ -117,6 +120,7 @@ class Gen:
     def __init__(self):
         self.lines = []
         self.label_n = 0
+        self.lds = []
 
     def __call__(self, s):
         self.lines.append(s)
@@ -127,6 +131,22 @@ class Gen:
     def new_label(self, stem):
         self.label_n += 1
         return f"L_{stem}_{self.label_n}_%="
+
+    # Outstanding LDS reads, oldest first.  LDS returns in order, so waiting for
+    # one read means allowing only the reads issued after it to be pending.
+    def lds_issue(self, tag):
+        self.lds.append(tag)
+
+    def lds_wait(self, tag):
+        if tag not in self.lds:
+            return
+        i = self.lds.index(tag)
+        self(f"s_waitcnt lgkmcnt({min(len(self.lds) - i - 1, 15)})")
+        del self.lds[:i + 1]
+
+    def lds_wait_all(self):
+        self("s_waitcnt lgkmcnt(0)")
+        self.lds = []
 
     def nops(self, n):
         while n > 0:
@@ -194,6 +214,19 @@ def kdma(g, i):
     g(f"global_load_lds_dwordx4 {vr(t)}, {sp(S_KDMA)}")
 
 
+def kdma_addr(g, i):
+    t = DTMP + i
+    g(f"v_min_u32 {vr(t)}, %[krow{i}], {s_(S_ROWLIM)}")
+    g(f"v_mad_u32_u24 {vr(t)}, {vr(t)}, %[ldkb], %[kcolb{i}]")
+
+
+def kdma_issue(g, i):
+    g(f"s_add_u32 {s_(S_M0)}, {s_(S_KST + 1)}, {i * 4096}")
+    g(f"s_add_u32 {s_(S_M0)}, {s_(S_M0)}, %[wave1k]")
+    set_m0(g, s_(S_M0))
+    g(f"global_load_lds_dwordx4 {vr(DTMP + i)}, {sp(S_KDMA)}")
+
+
 def vdma(g, i):
     g(f"s_add_u32 {s_(S_M0)}, {s_(S_VST + 1)}, {i * 4096}")
     g(f"s_add_u32 {s_(S_M0)}, {s_(S_M0)}, %[wave1k]")
@@ -206,11 +239,13 @@ def k_read(g, chunk, kk, stage_in_addr=True):
     the KADDR registers."""
     off = (chunk >> 2) * 8192 + kk * 4096
     g(f"ds_read_b128 {ar(kf_reg(chunk % 3, kk), 4)}, {vr(KADDR + (chunk & 3))} offset:{off}")
+    g.lds_issue(("k", chunk, kk))
 
 
 def v_read(g, f):
     grp, d = f // 4, f % 4
     g(f"ds_read_b128 {ar(vf_reg(f % 4), 4)}, {vr(VADDR + grp)} offset:{d * 4096}")
+    g.lds_issue(("v", f))
 
 
 def mfma_s(g, s_set, qb, kk, chunk):
@@ -237,7 +272,7 @@ def s_phase(g, s_set, items=None, dma=None, vreads_after=True):
     one per slot; dma: list of callables for the first slots."""
     slot = 0
     for c in range(8):
-        g(f"s_waitcnt lgkmcnt({2 if c < 7 else 0})")
+        g.lds_wait(("k", c, 1))
         for kk in range(2):
             for qb in range(2):
                 mfma_s(g, s_set, qb, kk, c)
@@ -254,14 +289,17 @@ def s_phase(g, s_set, items=None, dma=None, vreads_after=True):
                 slot += 1
 
 
-def o_phase(g, p_set, items=None):
-    """32 PV MFMAs with Vt fragments three ahead (the first three already issued)."""
+def o_phase(g, p_set, items=None, hooks=None):
+    """32 PV MFMAs with Vt fragments three ahead (the first three already issued);
+    hooks: {slot: callable} run before that slot's MFMA."""
     slot = 0
     for f in range(16):
         grp, d = f // 4, f % 4
-        pending_after = min(15 - f, 2)
-        g(f"s_waitcnt lgkmcnt({pending_after})")
         for qb in range(2):
+            if hooks and slot in hooks:
+                hooks[slot]()
+            if qb == 0:
+                g.lds_wait(("v", f))
             mfma_o(g, p_set, qb, d, grp, f % 4)
             if qb == 0 and f + 3 < 16:
                 v_read(g, f + 3)
@@ -355,36 +393,45 @@ def exact_rescale(g, s_set, p_set, kks, masked=False):
     g.nops(3)  # v_accvgpr_write -> MFMA srcC
 
 
-def tile(g, a, kt_label_last_other, first):
-    """One steady tile: current S/P set a, next set 1 - a."""
+def tile(g, a):
+    """One steady tile kt: scores of tile kt in S set a, S(kt+1) computed into set
+    1 - a.  Entered with the reads of K(kt+1) chunks 0 and 1 already issued.
+
+    The workgroup barrier that publishes this tile's DMA (K(kt+2), Vt(kt+1)) sits
+    inside phase 2, at OPTS["barrier_slot"]: the rest of phase 2 issues the next
+    tile's first K reads behind the PV MFMAs, so no LDS latency is exposed at the
+    tile boundary.  Vt therefore rotates through three stages: a wave past the
+    barrier may DMA Vt(kt+2) while another still reads Vt(kt)."""
     b = 1 - a
-    skip_kdma = g.new_label("nokdma")
     after_check = g.new_label("checked")
     resc = g.new_label("rescale")
-    # K read addresses of K(kt+1) (stage S_KST), Vt addresses of V(kt) (S_VST)
-    set_addrs(g, S_KST, S_VST)
-    k_read(g, 0, 0)
-    k_read(g, 0, 1)
-    k_read(g, 1, 0)
-    k_read(g, 1, 1)
-    # DMA of K(kt+2) when kt + 2 < nkt (row limit for the last tile), Vt(kt+1)
+    g.lds = [("k", 0, 0), ("k", 0, 1), ("k", 1, 0), ("k", 1, 1)]
+    for i in range(4):
+        g(f"v_add_u32 {vr(VADDR + i)}, {s_(S_VST)}, %[vbase{i}]")
+    # DMA of K(min(kt+2, nkt-1)) (past the last tile it refetches the last one
+    # into the stage of K(kt), which no wave reads any more) and of Vt(kt+1)
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 2")
     g(f"s_sub_u32 {s_(S_T1)}, %[nkt], 1")
+    g(f"s_min_u32 {s_(S_T0)}, {s_(S_T0)}, {s_(S_T1)}")
     g(f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_T1)}")
     g(f"s_cselect_b32 {s_(S_ROWLIM)}, {s_(S_VALID)}, {BN}")
     g(f"s_sub_u32 {s_(S_ROWLIM)}, {s_(S_ROWLIM)}, 1")
-    g(f"s_cmp_lt_u32 {s_(S_T0)}, %[nkt]")
-    g(f"s_cbranch_scc0 {skip_kdma}")
+    g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
+    g(f"s_mul_hi_u32 {s_(S_KDMA + 1)}, {s_(S_T0)}, %[ktile]")
+    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
+    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
     for i in range(4):
-        kdma(g, i)
-    g.label(skip_kdma)
-    for i in range(4):
-        vdma(g, i)
+        kdma_addr(g, i)
+    dmas = [(lambda i=i: kdma_issue(g, i)) for i in range(4)] + [(lambda i=i: vdma(g, i)) for i in range(4)]
+    if not OPTS["dma_slots"]:
+        for d in dmas:
+            d()
+        dmas = None
     # phase 1: S(kt+1) into set b || P(kt) keys 32..63 from set a
     g(f"v_mov_b32 {vr(RS1)}, 0")
     g(f"v_mov_b32 {vr(RS1 + 1)}, 0")
     items = make_items(g, pair_list(1), a, a, RS1)
-    s_phase(g, b, items=items)
+    s_phase(g, b, items=items, dma=dmas)
     # lazy-rescale check on tile kt: rsum = rs0 + rs1 (per lane), flag !(rsum <= 256)
     for qb in range(2):
         g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
@@ -399,26 +446,39 @@ def tile(g, a, kt_label_last_other, first):
         g(f"v_add_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(DTMP + qb)}")
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
     # phase 2: O += Vt(kt) P(kt) || P(kt+1) keys 0..31 from set b.  The wait
-    # covers both the VALU reads of the S(kt+1) results of the last MFMAs and the
-    # MFMA reads of the P(kt) just packed.
-    g.nops(18)
+    # covers the VALU reads of the S(kt+1) results of the last MFMAs (already
+    # three MFMAs old) and the MFMA reads of the P(kt) just packed.
+    g.nops(OPTS["p2wait"])
     items = make_items(g, pair_list(0), b, b, RS0)
-    o_phase(g, a, items=items)
-    # publish the DMA of this tile: own loads landed, then the workgroup barrier
-    g("s_waitcnt vmcnt(0)")
-    g("s_barrier")
-    # rotate: K stages swap, Vt stages swap, DMA bases advance, kt += 1
-    g(f"s_mov_b32 {s_(S_T0)}, {s_(S_KST)}")
-    g(f"s_mov_b32 {s_(S_KST)}, {s_(S_KST + 1)}")
-    g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T0)}")
-    g(f"s_mov_b32 {s_(S_T0)}, {s_(S_VST)}")
-    g(f"s_mov_b32 {s_(S_VST)}, {s_(S_VST + 1)}")
-    g(f"s_mov_b32 {s_(S_VST + 1)}, {s_(S_T0)}")
-    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[ktile]")
-    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
-    g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
-    g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
-    g(f"s_add_u32 {s_(S_KT)}, {s_(S_KT)}, 1")
+
+    def barrier():
+        # publish this tile's DMA: own loads landed, then the workgroup barrier
+        g("s_waitcnt vmcnt(0)")
+        g("s_barrier")
+        # rotate: K stages swap, Vt stages rotate, DMA base advances, kt += 1
+        g(f"s_mov_b32 {s_(S_T0)}, {s_(S_KST)}")
+        g(f"s_mov_b32 {s_(S_KST)}, {s_(S_KST + 1)}")
+        g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T0)}")
+        g(f"s_mov_b32 {s_(S_T0)}, {s_(S_VST)}")
+        g(f"s_mov_b32 {s_(S_VST)}, {s_(S_VST + 1)}")
+        g(f"s_mov_b32 {s_(S_VST + 1)}, {s_(S_V3)}")
+        g(f"s_mov_b32 {s_(S_V3)}, {s_(S_T0)}")
+        g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
+        g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
+        g(f"s_add_u32 {s_(S_KT)}, {s_(S_KT)}, 1")
+        for i in range(4):
+            g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
+
+    def next_reads(chunk):
+        return lambda: (k_read(g, chunk, 0), k_read(g, chunk, 1))
+    bs = OPTS["barrier_slot"]
+    if bs < 30:
+        o_phase(g, a, items=items, hooks={bs: barrier, bs + 1: next_reads(0), bs + 2: next_reads(1)})
+    else:
+        o_phase(g, a, items=items)
+        barrier()
+        next_reads(0)()
+        next_reads(1)()
     return resc, after_check
 
 
@@ -437,6 +497,7 @@ def last_tile(g, a):
     resc = g.new_label("lastresc")
     checked = g.new_label("lastchecked")
     g.nops(20)
+    g.lds_wait_all()
     set_addrs(g, S_KST, S_VST)
     for qb in range(2):
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
@@ -480,6 +541,7 @@ def prologue(g):
     g(f"s_add_u32 {s_(S_KST + 1)}, %[lds_k], {KSTAGE_BYTES}")
     g(f"s_mov_b32 {s_(S_VST)}, %[lds_v]")
     g(f"s_add_u32 {s_(S_VST + 1)}, %[lds_v], {VSTAGE_BYTES}")
+    g(f"s_add_u32 {s_(S_V3)}, %[lds_v], {2 * VSTAGE_BYTES}")
     g(f"s_mov_b32 {s_(S_KT)}, 0")
     g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
     # Q fragments straight into AGPRs
@@ -528,6 +590,7 @@ def prologue(g):
     # S(0) = K(0) Q^T into set A (K addresses of stage 0)
     for i in range(4):
         g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
+    g.lds = []
     k_read(g, 0, 0)
     k_read(g, 0, 1)
     k_read(g, 1, 0)
@@ -540,10 +603,18 @@ def prologue(g):
         g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(DTMP + 1)}")
     g("s_waitcnt vmcnt(0)")
     g("s_barrier")
-    # stage roles for tile 0: K(1) is read from stage 1 and K(2) goes to stage 0
+    # stage roles for tile 0: K(1) is read from stage 1 and K(2) goes to stage 0;
+    # the first reads of K(1) are issued here, as a tile expects
     g(f"s_mov_b32 {s_(S_T0)}, {s_(S_KST)}")
     g(f"s_mov_b32 {s_(S_KST)}, {s_(S_KST + 1)}")
     g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T0)}")
+    for i in range(4):
+        g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
+    g.lds = []
+    k_read(g, 0, 0)
+    k_read(g, 0, 1)
+    k_read(g, 1, 0)
+    k_read(g, 1, 1)
 
 
 def epilogue(g):
@@ -629,11 +700,11 @@ def generate():
     for it in items:
         it()
     g.label(loop)
-    ra, ba = tile(g, 0, last_b, True)
+    ra, ba = tile(g, 0)
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 1")
     g(f"s_cmp_ge_u32 {s_(S_T0)}, %[nkt]")
     g(f"s_cbranch_scc1 {last_b}")
-    rb, bb = tile(g, 1, last_a, False)
+    rb, bb = tile(g, 1)
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 1")
     g(f"s_cmp_ge_u32 {s_(S_T0)}, %[nkt]")
     g(f"s_cbranch_scc1 {last_a}")
@@ -652,7 +723,15 @@ def generate():
 
 def main(argv):
     here = os.path.dirname(os.path.abspath(__file__))
-    out = argv[1] if len(argv) > 1 else os.path.join(here, "attn_d128_body.inc")
+    args = [a for a in argv[1:] if not a.startswith("--")]
+    for a in argv[1:]:
+        if a.startswith("--p2wait="):
+            OPTS["p2wait"] = int(a.split("=", 1)[1])
+        elif a == "--dma-block":
+            OPTS["dma_slots"] = False
+        elif a.startswith("--barrier-slot="):
+            OPTS["barrier_slot"] = int(a.split("=", 1)[1])
+    out = args[0] if args else os.path.join(here, "attn_d128_body.inc")
     lines = generate()
     with open(out, "w") as f:
         f.write("// Generated by gen_attn_d128.py -- the instruction body of flash_fwd_d128.\n")

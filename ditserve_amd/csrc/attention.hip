@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
     const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
   constexpr int HD = 128, NW = 4, BM = 256;
   __shared__ u32x4_t Ks[2][BN * HD / 8];
-  __shared__ u32x4_t Vs[3][HD * 8];
+  __shared__ u32x4_t Vs[2][HD * 8];
   const int nb = gridDim.x;
   const int b = blockIdx.x;
   const int logical = (b & 7) * (nb >> 3) + (b >> 3);
@@ -728,22 +728,27 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
   const uint32_t ldkb = (uint32_t)(ldk * 2);
   // LDS read bases (bytes within a stage), as flash_fwd_kernel's kbase / vbase
   const int kr = kperm(l32), kg = (kr >> 1) & 7, vg = (l32 >> 1) & 7;
-  uint32_t kb[4], vb[4], krow[4], kcolb[4], voff[4];
+  // LDS read addresses (stage 0; the other stage is an immediate offset), K DMA
+  // source offsets (koffl: the last tile's, rows past the segment end reading its
+  // last row) and Vt DMA source offsets, per lane
+  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Ks[0][0];
+  const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Vs[0][0];
+  uint32_t kaddr[4], vaddr[4], koff[4], koffl[4], voff[4];
   const int lrow = lane >> 3;
   const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;
   const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    kb[i] = (uint32_t)(kr * 8 + ((i * 2 + hh) ^ kg)) * 16;
-    vb[i] = (uint32_t)(l32 * 8 + ((i * 2 + hh) ^ vg)) * 16;
+    kaddr[i] = lds_k + (uint32_t)(kr * 8 + ((i * 2 + hh) ^ kg)) * 16;
+    vaddr[i] = lds_v + (uint32_t)(l32 * 8 + ((i * 2 + hh) ^ vg)) * 16;
     const int g = i * NW + wave_u;
     const int grp = g / (BN / 8), r8 = g % (BN / 8);
-    krow[i] = (uint32_t)(r8 * 8 + lrow);
-    kcolb[i] = (uint32_t)(grp * 64 + ((r8 & 1) ? lsw1 : lsw0)) * 2;
+    const uint32_t krow = (uint32_t)(r8 * 8 + lrow);
+    const uint32_t kcolb = (uint32_t)(grp * 64 + ((r8 & 1) ? lsw1 : lsw0)) * 2;
+    koff[i] = krow * ldkb + kcolb;
+    koffl[i] = min(krow, (uint32_t)(valid_last - 1)) * ldkb + kcolb;
     voff[i] = (uint32_t)((int64_t)(g * 8 + lrow) * vt_ld + ((g & 1) ? lsw1 : lsw0)) * 2;
   }
-  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Ks[0][0];
-  const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Vs[0][0];
   const uint32_t wave1k = (uint32_t)wave_u * 1024u;
   const uint32_t xaddr = (uint32_t)((lane ^ 32) * 4);
   const uint32_t hh8 = (uint32_t)(hh * 8);
@@ -762,14 +767,14 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
       : [qbase] "s"(su64(qbase)), [qoff0] "v"(qoff0), [qoff1] "v"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),
         [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),
         [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),
-        [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [ldkb] "s"(su(ldkb)),
+        [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)),
         [wave1k] "s"(su(wave1k)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)),
         [obase_lo] "s"(su((uint32_t)obase)), [obase_hi] "s"(su((uint32_t)(obase >> 32))),
-        [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)), [kbase0] "v"(kb[0]), [kbase1] "v"(kb[1]),
-        [kbase2] "v"(kb[2]), [kbase3] "v"(kb[3]), [vbase0] "v"(vb[0]), [vbase1] "v"(vb[1]), [vbase2] "v"(vb[2]),
-        [vbase3] "v"(vb[3]), [krow0] "v"(krow[0]), [krow1] "v"(krow[1]), [krow2] "v"(krow[2]),
-        [krow3] "v"(krow[3]), [kcolb0] "v"(kcolb[0]), [kcolb1] "v"(kcolb[1]), [kcolb2] "v"(kcolb[2]),
-        [kcolb3] "v"(kcolb[3]), [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]),
+        [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)), [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]),
+        [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]), [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]),
+        [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]), [koff0] "v"(koff[0]), [koff1] "v"(koff[1]),
+        [koff2] "v"(koff[2]), [koff3] "v"(koff[3]), [koffl0] "v"(koffl[0]), [koffl1] "v"(koffl[1]),
+        [koffl2] "v"(koffl[2]), [koffl3] "v"(koffl[3]), [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]),
         [voff3] "v"(voff[3]), [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0),
         [qrow1] "v"(qrow1)
       : DITK_D128_CLOBBERS "vcc", "scc", "memory");

@@ -16,20 +16,23 @@ registers are assigned here by hand:
   VGPR v202..v203  rs1[qb]   row sums of keys 32..63
   VGPR v204..v205  negm[qb]  minus the running max (log2 units)
   VGPR v206..v207  l[qb]     running softmax denominators
-  VGPR v208..v211  K fragment LDS read addresses (per chunk residue c % 4)
-  VGPR v212..v215  Vt fragment LDS read addresses (per key group g)
-  VGPR v216..v219  DMA address temporaries
+  VGPR v208..v211  K DMA source offsets (switched to the clamped ones for the
+                   last tile)
+  VGPR v212..v215  temporaries
   AGPR a0..a127    O^T accumulators [qb][d] (16 each)
   AGPR a128..a191  Q fragments [qb][c] (4 each)
   AGPR a192..a215  K fragment ring: 3 chunks x 2 (kk)
-  AGPR a216..a231  Vt fragment ring: 4 fragments
+  AGPR a216..a239  Vt fragment ring: 6 fragments
+The LDS read addresses and DMA offsets that never change are compiler-placed
+input operands; the K and Vt stages alternate with the tile parity, so the
+stage is an immediate offset of each LDS read and DMA.
 
 Per 64-key tile kt the wave (queries q0..q0+63 of one (segment, head)) runs
   phase 1: S(kt+1) = K(kt+1) Q^T    (32 MFMAs)  ||  P(kt) keys 32..63 (VALU)
   check:   lazy-rescale test on the row sums of P(kt)
   phase 2: O += Vt(kt) P(kt)        (32 MFMAs)  ||  P(kt+1) keys 0..31 (VALU)
 with one VALU half-item per MFMA slot, K fragments read two chunks ahead and
-Vt fragments three fragments ahead, and the next tiles' K and Vt streamed into
+Vt fragments four fragments ahead, and the next tiles' K and Vt streamed into
 LDS by direct global->LDS DMA.  The arithmetic per score, the order of every
 row sum and the rescale rule are those of the C++ kernel
 (flash_fwd_kernel<128, 8, 1>), so the two agree bitwise.
@@ -38,7 +41,8 @@ Hazards the hardware does not interlock are covered explicitly: an s_nop before
 VALU reads of MFMA results and before MFMAs read AGPRs written by
 v_accvgpr_write, an s_nop between an M0 write and the DMA that reads it.
 
-Usage: python gen_attn_d128.py [out.inc]  (writes attn_d128_body.inc beside it)
+Usage: python gen_attn_d128.py [out.inc]  (default attn_d128_body.inc beside this
+file; attn_d128_clobbers.h is written beside the output)
 """
 import os
 import sys
@@ -49,28 +53,26 @@ S_SET = (0, 64)
 P_SET = (128, 160)
 TMP = 192
 RS0, RS1, NEGM, LRUN = 200, 202, 204, 206
-KADDR, VADDR, DTMP = 208, 212, 216
+KOFF, DTMP = 208, 212
 O_A, Q_A, KF_A, VF_A = 0, 128, 192, 216
-LAST_VGPR, LAST_AGPR = 219, 231
+VRING = 6        # Vt fragment ring (read four fragments ahead)
+LAST_VGPR, LAST_AGPR = 215, VF_A + 4 * VRING - 1
 
 # scalar registers owned by the body (all callee state lives in these)
-S_KDMA = 60      # s[60:61] K DMA base (bytes) of tile kt+2
+S_KDMA = 60      # s[60:61] K DMA base (bytes) of tile min(kt+2, nkt-1)
 S_VDMA = 62      # s[62:63] Vt DMA base (bytes) of tile kt+1
-S_KST = 64       # s64 LDS base of the K stage read this tile, s65 the DMA stage
-S_VST = 66       # s66 Vt stage read this tile, s67 Vt DMA stage
-S_KT = 68        # s68 tile index kt
-S_ROWLIM = 69    # s69 last valid row of the K tile being DMA'd
-S_T0, S_T1, S_T2, S_T3 = 70, 71, 72, 73
-S_CMP = 74       # s[74:75] compare mask
-S_EXEC = 76      # s[76:77] saved exec
-S_VALID = 78     # s78 valid keys of the last tile
-S_M0 = 79        # s79 M0 staging
-S_V3 = 80        # s80 the third Vt stage (read two tiles from now)
-SGPRS = list(range(60, 81))
+S_KW = 64        # s64 LDS K base + this wave's 1 KiB DMA slice
+S_VW = 65        # s65 LDS Vt base + this wave's 1 KiB DMA slice
+S_KT = 66        # s66 tile index kt
+S_NKT1 = 67      # s67 nkt - 1
+S_T0, S_T1 = 68, 69
+S_CMP = 70       # s[70:71] compare mask
+S_EXEC = 72      # s[72:73] saved exec
+S_VALID = 74     # s74 valid keys of the last tile
+S_THR = 75       # s75 the lazy-rescale threshold 256.0
+SGPRS = list(range(60, 76))
 
 BN, HD = 64, 128
-# schedule options (the defaults are the shipped schedule)
-OPTS = {"p2wait": 2, "dma_slots": True, "barrier_slot": 32}
 KSTAGE_BYTES = BN * HD * 2     # 16 KiB
 VSTAGE_BYTES = HD * BN * 2     # 16 KiB
 
@@ -181,7 +183,8 @@ def item_order(n):
 
 def emit_half(g, half, pi, pair, s_set, p_set, rs_base):
     """One half-item: 'a' = two fma + two exp2 into the temp ring, 'b' = pack into
-    P, and the row sum rs += (p0 + p1)."""
+    P, and the row sum rs += (p0 + p1).  The first pair of a query block starts
+    the sum (rs = p0 + p1, the same value as 0 + (p0 + p1))."""
     qb, kk, j, e = pair
     t0 = TMP + 2 * (pi % 4)
     t1 = t0 + 1
@@ -193,58 +196,67 @@ def emit_half(g, half, pi, pair, s_set, p_set, rs_base):
         g(f"v_exp_f32 {vr(t1)}, {vr(t1)}")
     else:
         g(f"v_cvt_pk_bf16_f32 {vr(p_reg(p_set, qb, kk * 2 + j, e))}, {vr(t0)}, {vr(t1)}")
-        g(f"v_add_f32 {vr(t0)}, {vr(t0)}, {vr(t1)}")
-        g(f"v_add_f32 {vr(rs_base + qb)}, {vr(rs_base + qb)}, {vr(t0)}")
+        if j == 0 and e == 0:
+            g(f"v_add_f32 {vr(rs_base + qb)}, {vr(t0)}, {vr(t1)}")
+        else:
+            g(f"v_add_f32 {vr(t0)}, {vr(t0)}, {vr(t1)}")
+            g(f"v_add_f32 {vr(rs_base + qb)}, {vr(rs_base + qb)}, {vr(t0)}")
 
 
-def set_m0(g, sreg_expr):
-    g(f"s_mov_b32 m0, {sreg_expr}")
-    g("s_nop 0")
+# LDS DMA: M0 carries this wave's LDS destination (stage base + 1 KiB slice +
+# 4 KiB per instruction); each lane moves 16 bytes.  The M0 write and the DMA
+# that reads it are one instruction apart at least (one wait state).
+def kdma_m0(g, i, stage):
+    g(f"s_add_u32 m0, {s_(S_KW)}, {stage * KSTAGE_BYTES + i * 4096}")
 
 
-def kdma(g, i):
-    """DMA instruction i (0..3) of this wave for the K tile at S_KDMA into the K
-    DMA stage: rows min(krow_i, rowlim), 16 bytes per lane."""
-    t = DTMP + i
-    g(f"v_min_u32 {vr(t)}, %[krow{i}], {s_(S_ROWLIM)}")
-    g(f"v_mad_u32_u24 {vr(t)}, {vr(t)}, %[ldkb], %[kcolb{i}]")
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_KST + 1)}, {i * 4096}")
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_M0)}, %[wave1k]")
-    set_m0(g, s_(S_M0))
-    g(f"global_load_lds_dwordx4 {vr(t)}, {sp(S_KDMA)}")
+def kdma_go(g, i):
+    g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KDMA)}")
 
 
-def kdma_addr(g, i):
-    t = DTMP + i
-    g(f"v_min_u32 {vr(t)}, %[krow{i}], {s_(S_ROWLIM)}")
-    g(f"v_mad_u32_u24 {vr(t)}, {vr(t)}, %[ldkb], %[kcolb{i}]")
+def vdma_m0(g, i, stage):
+    g(f"s_add_u32 m0, {s_(S_VW)}, {stage * VSTAGE_BYTES + i * 4096}")
 
 
-def kdma_issue(g, i):
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_KST + 1)}, {i * 4096}")
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_M0)}, %[wave1k]")
-    set_m0(g, s_(S_M0))
-    g(f"global_load_lds_dwordx4 {vr(DTMP + i)}, {sp(S_KDMA)}")
-
-
-def vdma(g, i):
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_VST + 1)}, {i * 4096}")
-    g(f"s_add_u32 {s_(S_M0)}, {s_(S_M0)}, %[wave1k]")
-    set_m0(g, s_(S_M0))
+def vdma_go(g, i):
     g(f"global_load_lds_dwordx4 %[voff{i}], {sp(S_VDMA)}")
 
 
-def k_read(g, chunk, kk, stage_in_addr=True):
-    """ds_read of K fragment (chunk, kk) from the K stage whose base is folded into
-    the KADDR registers."""
-    off = (chunk >> 2) * 8192 + kk * 4096
-    g(f"ds_read_b128 {ar(kf_reg(chunk % 3, kk), 4)}, {vr(KADDR + (chunk & 3))} offset:{off}")
+def kdma_block(g, stage):
+    for i in range(4):
+        kdma_m0(g, i, stage)
+        g("s_nop 0")
+        kdma_go(g, i)
+
+
+def vdma_block(g, stage):
+    for i in range(4):
+        vdma_m0(g, i, stage)
+        g("s_nop 0")
+        vdma_go(g, i)
+
+
+def clamp_koff(g, cmp):
+    """K DMA offsets of the last tile (rows past the end read the last row) when
+    the scalar compare `cmp` holds."""
+    skip = g.new_label("noclamp")
+    g(cmp)
+    g(f"s_cbranch_scc0 {skip}")
+    for i in range(4):
+        g(f"v_mov_b32 {vr(KOFF + i)}, %[koffl{i}]")
+    g.label(skip)
+
+
+def k_read(g, chunk, kk, stage):
+    """ds_read of K fragment (chunk, kk) of K stage `stage`."""
+    off = stage * KSTAGE_BYTES + (chunk >> 2) * 8192 + kk * 4096
+    g(f"ds_read_b128 {ar(kf_reg(chunk % 3, kk), 4)}, %[kaddr{chunk & 3}] offset:{off}")
     g.lds_issue(("k", chunk, kk))
 
 
-def v_read(g, f):
+def v_read(g, f, stage):
     grp, d = f // 4, f % 4
-    g(f"ds_read_b128 {ar(vf_reg(f % 4), 4)}, {vr(VADDR + grp)} offset:{d * 4096}")
+    g(f"ds_read_b128 {ar(vf_reg(f % VRING), 4)}, %[vaddr{grp}] offset:{stage * VSTAGE_BYTES + d * 4096}")
     g.lds_issue(("v", f))
 
 
@@ -259,50 +271,46 @@ def mfma_o(g, p_set, qb, d, grp, ring):
     g(f"v_mfma_f32_32x32x16_bf16 {ar(o, 16)}, {ar(vf_reg(ring), 4)}, {vr(p_reg(p_set, qb, grp), 4)}, {ar(o, 16)}")
 
 
-def set_addrs(g, k_stage_sreg, v_stage_sreg):
-    for i in range(4):
-        g(f"v_add_u32 {vr(KADDR + i)}, {s_(k_stage_sreg)}, %[kbase{i}]")
-    for i in range(4):
-        g(f"v_add_u32 {vr(VADDR + i)}, {s_(v_stage_sreg)}, %[vbase{i}]")
-
-
-def s_phase(g, s_set, items=None, dma=None, vreads_after=True):
-    """32 S MFMAs (S(kt+1) into s_set) with K fragments two chunks ahead; the
-    first two chunks' reads must already be issued.  items: list of callables,
-    one per slot; dma: list of callables for the first slots."""
+def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None):
+    """32 S MFMAs (into s_set) with K fragments of K stage kstage read two chunks
+    ahead; the first two chunks' reads must already be issued.  vstage: issue the
+    first four Vt reads of that stage after the last chunk's first MFMA.  items:
+    one callable per slot; dma: (before, after) callables around the MFMA of the
+    first slots."""
     slot = 0
     for c in range(8):
         g.lds_wait(("k", c, 1))
         for kk in range(2):
             for qb in range(2):
+                d = dma[slot] if dma is not None and slot < len(dma) else None
+                if d:
+                    d[0]()
                 mfma_s(g, s_set, qb, kk, c)
                 if kk == 0 and qb == 0 and c + 2 < 8:
-                    k_read(g, c + 2, 0)
-                    k_read(g, c + 2, 1)
-                if kk == 0 and qb == 0 and c == 7 and vreads_after:
-                    for f in range(3):
-                        v_read(g, f)
-                if dma is not None and slot < len(dma):
-                    dma[slot]()
+                    k_read(g, c + 2, 0, kstage)
+                    k_read(g, c + 2, 1, kstage)
+                if kk == 0 and qb == 0 and c == 7 and vstage is not None:
+                    for f in range(4):
+                        v_read(g, f, vstage)
+                if d:
+                    d[1]()
                 if items is not None:
                     items[slot]()
                 slot += 1
 
 
-def o_phase(g, p_set, items=None, hooks=None):
-    """32 PV MFMAs with Vt fragments three ahead (the first three already issued);
-    hooks: {slot: callable} run before that slot's MFMA."""
+def o_phase(g, p_set, vstage, items=None):
+    """32 PV MFMAs with Vt fragments of stage vstage four ahead (the first four
+    already issued), waited for in pairs."""
     slot = 0
     for f in range(16):
         grp, d = f // 4, f % 4
         for qb in range(2):
-            if hooks and slot in hooks:
-                hooks[slot]()
-            if qb == 0:
-                g.lds_wait(("v", f))
-            mfma_o(g, p_set, qb, d, grp, f % 4)
-            if qb == 0 and f + 3 < 16:
-                v_read(g, f + 3)
+            if qb == 0 and f % 2 == 0:
+                g.lds_wait(("v", f + 1))
+            mfma_o(g, p_set, qb, d, grp, f % VRING)
+            if qb == 0 and f + 4 < 16:
+                v_read(g, f + 4, vstage)
             if items is not None:
                 items[slot]()
             slot += 1
@@ -394,111 +402,80 @@ def exact_rescale(g, s_set, p_set, kks, masked=False):
 
 
 def tile(g, a):
-    """One steady tile kt: scores of tile kt in S set a, S(kt+1) computed into set
-    1 - a.  Entered with the reads of K(kt+1) chunks 0 and 1 already issued.
+    """One steady tile kt (kt % 2 == a): scores of tile kt in S set a, S(kt+1)
+    computed into set b = 1 - a.  Entered with the reads of K(kt+1) chunks 0 and
+    1 already issued.
 
-    The workgroup barrier that publishes this tile's DMA (K(kt+2), Vt(kt+1)) sits
-    inside phase 2, at OPTS["barrier_slot"]: the rest of phase 2 issues the next
-    tile's first K reads behind the PV MFMAs, so no LDS latency is exposed at the
-    tile boundary.  Vt therefore rotates through three stages: a wave past the
-    barrier may DMA Vt(kt+2) while another still reads Vt(kt)."""
+    LDS stages are fixed by parity: K(kt+1) is read from K stage b while K(tile
+    min(kt+2, nkt-1)) is DMA'd into K stage a (K(kt) is read by no wave any
+    more); Vt(kt) is read from Vt stage a while Vt(kt+1) is DMA'd into stage b.
+    The workgroup barrier at the end of the tile publishes both DMAs."""
     b = 1 - a
     after_check = g.new_label("checked")
     resc = g.new_label("rescale")
     g.lds = [("k", 0, 0), ("k", 0, 1), ("k", 1, 0), ("k", 1, 1)]
-    for i in range(4):
-        g(f"v_add_u32 {vr(VADDR + i)}, {s_(S_VST)}, %[vbase{i}]")
-    # DMA of K(min(kt+2, nkt-1)) (past the last tile it refetches the last one
-    # into the stage of K(kt), which no wave reads any more) and of Vt(kt+1)
+    # K DMA base of tile min(kt+2, nkt-1); the last tile's rows past the end clamp
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 2")
-    g(f"s_sub_u32 {s_(S_T1)}, %[nkt], 1")
-    g(f"s_min_u32 {s_(S_T0)}, {s_(S_T0)}, {s_(S_T1)}")
-    g(f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_T1)}")
-    g(f"s_cselect_b32 {s_(S_ROWLIM)}, {s_(S_VALID)}, {BN}")
-    g(f"s_sub_u32 {s_(S_ROWLIM)}, {s_(S_ROWLIM)}, 1")
+    g(f"s_min_u32 {s_(S_T0)}, {s_(S_T0)}, {s_(S_NKT1)}")
     g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
     g(f"s_mul_hi_u32 {s_(S_KDMA + 1)}, {s_(S_T0)}, %[ktile]")
     g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
     g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
-    for i in range(4):
-        kdma_addr(g, i)
-    dmas = [(lambda i=i: kdma_issue(g, i)) for i in range(4)] + [(lambda i=i: vdma(g, i)) for i in range(4)]
-    if not OPTS["dma_slots"]:
-        for d in dmas:
-            d()
-        dmas = None
+    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
+    dmas = ([(lambda i=i: kdma_m0(g, i, a), lambda i=i: kdma_go(g, i)) for i in range(4)] +
+            [(lambda i=i: vdma_m0(g, i, b), lambda i=i: vdma_go(g, i)) for i in range(4)])
     # phase 1: S(kt+1) into set b || P(kt) keys 32..63 from set a
-    g(f"v_mov_b32 {vr(RS1)}, 0")
-    g(f"v_mov_b32 {vr(RS1 + 1)}, 0")
     items = make_items(g, pair_list(1), a, a, RS1)
-    s_phase(g, b, items=items, dma=dmas)
+    s_phase(g, b, kstage=b, vstage=a, items=items, dma=dmas)
     # lazy-rescale check on tile kt: rsum = rs0 + rs1 (per lane), flag !(rsum <= 256)
     for qb in range(2):
         g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
-    g(f"s_mov_b32 {s_(S_T2)}, 0x43800000")
-    g(f"v_cmp_nge_f32 vcc, {s_(S_T2)}, {vr(DTMP)}")
-    g(f"v_cmp_nge_f32_e64 {sp(S_CMP)}, {s_(S_T2)}, {vr(DTMP + 1)}")
+    g(f"v_cmp_nge_f32 vcc, {s_(S_THR)}, {vr(DTMP)}")
+    g(f"v_cmp_nge_f32_e64 {sp(S_CMP)}, {s_(S_THR)}, {vr(DTMP + 1)}")
     g(f"s_or_b64 vcc, vcc, {sp(S_CMP)}")
     g(f"s_cbranch_vccnz {resc}")
     g.label(after_check)
     for qb in range(2):
-        g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
         g(f"v_add_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(DTMP + qb)}")
-        g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
     # phase 2: O += Vt(kt) P(kt) || P(kt+1) keys 0..31 from set b.  The wait
     # covers the VALU reads of the S(kt+1) results of the last MFMAs (already
     # three MFMAs old) and the MFMA reads of the P(kt) just packed.
-    g.nops(OPTS["p2wait"])
+    g.nops(2)
     items = make_items(g, pair_list(0), b, b, RS0)
-
-    def barrier():
-        # publish this tile's DMA: own loads landed, then the workgroup barrier
-        g("s_waitcnt vmcnt(0)")
-        g("s_barrier")
-        # rotate: K stages swap, Vt stages rotate, DMA base advances, kt += 1
-        g(f"s_mov_b32 {s_(S_T0)}, {s_(S_KST)}")
-        g(f"s_mov_b32 {s_(S_KST)}, {s_(S_KST + 1)}")
-        g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T0)}")
-        g(f"s_mov_b32 {s_(S_T0)}, {s_(S_VST)}")
-        g(f"s_mov_b32 {s_(S_VST)}, {s_(S_VST + 1)}")
-        g(f"s_mov_b32 {s_(S_VST + 1)}, {s_(S_V3)}")
-        g(f"s_mov_b32 {s_(S_V3)}, {s_(S_T0)}")
-        g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
-        g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
-        g(f"s_add_u32 {s_(S_KT)}, {s_(S_KT)}, 1")
-        for i in range(4):
-            g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
-
-    def next_reads(chunk):
-        return lambda: (k_read(g, chunk, 0), k_read(g, chunk, 1))
-    bs = OPTS["barrier_slot"]
-    if bs < 30:
-        o_phase(g, a, items=items, hooks={bs: barrier, bs + 1: next_reads(0), bs + 2: next_reads(1)})
-    else:
-        o_phase(g, a, items=items)
-        barrier()
-        next_reads(0)()
-        next_reads(1)()
+    o_phase(g, a, vstage=a, items=items)
+    # publish this tile's DMA: own loads landed, then the workgroup barrier
+    g("s_waitcnt vmcnt(0)")
+    g("s_barrier")
+    g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
+    g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
+    g(f"s_add_u32 {s_(S_KT)}, {s_(S_KT)}, 1")
+    # the next tile's first K reads: K(kt+2), in stage a
+    for c in range(2):
+        k_read(g, c, 0, a)
+        k_read(g, c, 1, a)
     return resc, after_check
 
 
 def rescale_block(g, a, resc, back):
-    """Out-of-line rescale of tile kt (scores still in set a, P(kt) in P set a)."""
+    """Out-of-line rescale of tile kt (scores still in set a, P(kt) in P set a);
+    returns with the tile's row sums in DTMP like the common path."""
     g.label(resc)
     exact_rescale(g, a, a, (0, 1))
+    for qb in range(2):
+        g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
     g(f"s_branch {back}")
 
 
 def last_tile(g, a):
-    """The last key tile (scores in set a): P of all 64 keys against m with keys
-    past the segment end out of the row sums, the rescale test, then O += Vt P."""
+    """The last key tile (kt % 2 == a, scores in set a): P of all 64 keys against
+    m with keys past the segment end out of the row sums, the rescale test, then
+    O += Vt P."""
     full = g.new_label("fullrs")
     done_rs = g.new_label("rsdone")
     resc = g.new_label("lastresc")
     checked = g.new_label("lastchecked")
     g.nops(20)
     g.lds_wait_all()
-    set_addrs(g, S_KST, S_VST)
     for qb in range(2):
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
     g(f"s_cmp_eq_u32 {s_(S_VALID)}, {BN}")
@@ -510,9 +487,8 @@ def last_tile(g, a):
     for qb in range(2):
         softmax_tile(g, a, a, qb, (0, 1), RS0, masked=False)
     g.label(done_rs)
-    g(f"s_mov_b32 {s_(S_T2)}, 0x43800000")
-    g(f"v_cmp_nge_f32 vcc, {s_(S_T2)}, {vr(RS0)}")
-    g(f"v_cmp_nge_f32_e64 {sp(S_CMP)}, {s_(S_T2)}, {vr(RS0 + 1)}")
+    g(f"v_cmp_nge_f32 vcc, {s_(S_THR)}, {vr(RS0)}")
+    g(f"v_cmp_nge_f32_e64 {sp(S_CMP)}, {s_(S_THR)}, {vr(RS0 + 1)}")
     g(f"s_or_b64 vcc, vcc, {sp(S_CMP)}")
     g(f"s_cbranch_vccz {checked}")
     # rescale against the exact tile max (masked sums)
@@ -526,24 +502,21 @@ def last_tile(g, a):
     for qb in range(2):
         g(f"v_add_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(RS0 + qb)}")
     g("s_nop 2")
-    for f in range(3):
-        v_read(g, f)
-    o_phase(g, a, items=None)
+    for f in range(4):
+        v_read(g, f, a)
+    o_phase(g, a, vstage=a, items=None)
 
 
 def prologue(g):
     # scalar state
-    g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
-    g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
     g(f"s_mov_b32 {s_(S_VDMA)}, %[vdma_lo]")
     g(f"s_mov_b32 {s_(S_VDMA + 1)}, %[vdma_hi]")
-    g(f"s_mov_b32 {s_(S_KST)}, %[lds_k]")
-    g(f"s_add_u32 {s_(S_KST + 1)}, %[lds_k], {KSTAGE_BYTES}")
-    g(f"s_mov_b32 {s_(S_VST)}, %[lds_v]")
-    g(f"s_add_u32 {s_(S_VST + 1)}, %[lds_v], {VSTAGE_BYTES}")
-    g(f"s_add_u32 {s_(S_V3)}, %[lds_v], {2 * VSTAGE_BYTES}")
+    g(f"s_add_u32 {s_(S_KW)}, %[lds_k], %[wave1k]")
+    g(f"s_add_u32 {s_(S_VW)}, %[lds_v], %[wave1k]")
     g(f"s_mov_b32 {s_(S_KT)}, 0")
+    g(f"s_sub_u32 {s_(S_NKT1)}, %[nkt], 1")
     g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
+    g(f"s_mov_b32 {s_(S_THR)}, 0x43800000")
     # Q fragments straight into AGPRs
     for qb in range(2):
         for c in range(8):
@@ -555,47 +528,33 @@ def prologue(g):
         g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
         g(f"v_mov_b32 {vr(RS1 + qb)}, 0")
-    # K(0) into stage 0 (DMA stage register temporarily = stage 0)
-    g(f"s_cmp_eq_u32 %[nkt], 1")
-    g(f"s_cselect_b32 {s_(S_ROWLIM)}, {s_(S_VALID)}, {BN}")
-    g(f"s_sub_u32 {s_(S_ROWLIM)}, {s_(S_ROWLIM)}, 1")
-    g(f"s_mov_b32 {s_(S_T3)}, {s_(S_KST + 1)}")
-    g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_KST)}")
     for i in range(4):
-        kdma(g, i)
-    g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T3)}")
+        g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
+    # K(0) into K stage 0 (clamped when it is the last tile)
+    g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
+    g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
+    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
+    kdma_block(g, 0)
     g("s_waitcnt vmcnt(0)")
     g("s_barrier")
-    # K(1) into stage 1 when nkt > 1; Vt(0) into Vt stage 0
+    # K(1) into K stage 1 when nkt > 1 (clamped when last); Vt(0) into Vt stage 0
     no_k1 = g.new_label("nok1")
+    g(f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
+    g(f"s_cbranch_scc1 {no_k1}")
     g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[ktile]")
     g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
-    g(f"s_cmp_le_u32 %[nkt], 1")
-    g(f"s_cbranch_scc1 {no_k1}")
-    g(f"s_cmp_eq_u32 %[nkt], 2")
-    g(f"s_cselect_b32 {s_(S_ROWLIM)}, {s_(S_VALID)}, {BN}")
-    g(f"s_sub_u32 {s_(S_ROWLIM)}, {s_(S_ROWLIM)}, 1")
-    for i in range(4):
-        kdma(g, i)
+    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 1")
+    kdma_block(g, 1)
     g.label(no_k1)
-    g(f"s_mov_b32 {s_(S_T3)}, {s_(S_VST + 1)}")
-    g(f"s_mov_b32 {s_(S_VST + 1)}, {s_(S_VST)}")
-    for i in range(4):
-        vdma(g, i)
-    g(f"s_mov_b32 {s_(S_VST + 1)}, {s_(S_T3)}")
+    vdma_block(g, 0)
     g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
     g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
-    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[ktile]")
-    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
-    # S(0) = K(0) Q^T into set A (K addresses of stage 0)
-    for i in range(4):
-        g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
+    # S(0) = K(0) Q^T into set A
     g.lds = []
-    k_read(g, 0, 0)
-    k_read(g, 0, 1)
-    k_read(g, 1, 0)
-    k_read(g, 1, 1)
-    s_phase(g, 0, items=None, dma=None, vreads_after=False)
+    for c in range(2):
+        k_read(g, c, 0, 0)
+        k_read(g, c, 1, 0)
+    s_phase(g, 0, kstage=0)
     g.nops(20)
     # m = exact max of tile 0
     for qb in range(2):
@@ -603,18 +562,11 @@ def prologue(g):
         g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(DTMP + 1)}")
     g("s_waitcnt vmcnt(0)")
     g("s_barrier")
-    # stage roles for tile 0: K(1) is read from stage 1 and K(2) goes to stage 0;
-    # the first reads of K(1) are issued here, as a tile expects
-    g(f"s_mov_b32 {s_(S_T0)}, {s_(S_KST)}")
-    g(f"s_mov_b32 {s_(S_KST)}, {s_(S_KST + 1)}")
-    g(f"s_mov_b32 {s_(S_KST + 1)}, {s_(S_T0)}")
-    for i in range(4):
-        g(f"v_add_u32 {vr(KADDR + i)}, {s_(S_KST)}, %[kbase{i}]")
+    # tile 0 reads K(1) from K stage 1; its first reads are issued here
     g.lds = []
-    k_read(g, 0, 0)
-    k_read(g, 0, 1)
-    k_read(g, 1, 0)
-    k_read(g, 1, 1)
+    for c in range(2):
+        k_read(g, c, 0, 1)
+        k_read(g, c, 1, 1)
 
 
 def epilogue(g):
@@ -701,14 +653,12 @@ def generate():
         it()
     g.label(loop)
     ra, ba = tile(g, 0)
-    g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 1")
-    g(f"s_cmp_ge_u32 {s_(S_T0)}, %[nkt]")
+    g(f"s_cmp_ge_u32 {s_(S_KT)}, {s_(S_NKT1)}")
     g(f"s_cbranch_scc1 {last_b}")
     rb, bb = tile(g, 1)
-    g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 1")
-    g(f"s_cmp_ge_u32 {s_(S_T0)}, %[nkt]")
-    g(f"s_cbranch_scc1 {last_a}")
-    g(f"s_branch {loop}")
+    g(f"s_cmp_lt_u32 {s_(S_KT)}, {s_(S_NKT1)}")
+    g(f"s_cbranch_scc1 {loop}")
+    g(f"s_branch {last_a}")
     rescale_block(g, 0, ra, ba)
     rescale_block(g, 1, rb, bb)
     g.label(last_a)
@@ -721,23 +671,25 @@ def generate():
     return g.lines
 
 
+def clobbers():
+    regs = ([f"v{i}" for i in range(LAST_VGPR + 1)] + [f"a{i}" for i in range(LAST_AGPR + 1)] +
+            [f"s{i}" for i in SGPRS])
+    rows = [", ".join(f'"{r}"' for r in regs[i:i + 16]) for i in range(0, len(regs), 16)]
+    return ("// Registers the generated flash_fwd_d128 body owns (gen_attn_d128.py register map).\n"
+            "#define DITK_D128_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
+
+
 def main(argv):
     here = os.path.dirname(os.path.abspath(__file__))
-    args = [a for a in argv[1:] if not a.startswith("--")]
-    for a in argv[1:]:
-        if a.startswith("--p2wait="):
-            OPTS["p2wait"] = int(a.split("=", 1)[1])
-        elif a == "--dma-block":
-            OPTS["dma_slots"] = False
-        elif a.startswith("--barrier-slot="):
-            OPTS["barrier_slot"] = int(a.split("=", 1)[1])
-    out = args[0] if args else os.path.join(here, "attn_d128_body.inc")
+    out = argv[1] if len(argv) > 1 else os.path.join(here, "attn_d128_body.inc")
     lines = generate()
     with open(out, "w") as f:
         f.write("// Generated by gen_attn_d128.py -- the instruction body of flash_fwd_d128.\n")
         for line in lines:
             esc = line.replace("\\", "\\\\").replace('"', '\\"')
             f.write(f'"{esc}\\n"\n')
+    with open(os.path.join(os.path.dirname(os.path.abspath(out)), "attn_d128_clobbers.h"), "w") as f:
+        f.write(clobbers())
     return 0
 
 

@@ -14,10 +14,12 @@ scheduler step).
 Every call launches on the caller's current stream and allocates only through
 the stream-aware caching allocator; packets carry ``record_stream`` on every
 device object they hold.  So the reference's interleaved mode -- the uncond
-branch's blocks on a side stream (block.py:237-300) -- runs these blocks through
-its generic ``_forward_block`` path (the ditk model exposes no diffusers
-sublayers) and gives the same results as sequential execution.  One GPU: a
-layout or group of more than one rank is rejected.
+branch's blocks on a side stream (block.py:237-300) -- gives the same results as
+sequential execution when it sends ditk packets through its generic
+``_forward_block`` path (block.py:254-266), i.e. ``engine.forward_block``: its
+sublayer path would run the diffusers block's own modules on the packet, whose
+layout (token-major ``[T, D]`` hidden rows, angle-table rotary) is ditk's.  One
+GPU: a layout or group of more than one rank is rejected.
 """
 import torch
 

@@ -73,8 +73,3 @@ def packed_plan(img_counts, txt_counts):
         "total_joint": cu_joint[-1],
     }
 
-
-def wan_tokens(grid):
-    """Tokens of a Wan latent grid (F', H', W') after the 1x2x2 patchify."""
-    f, h, w = grid
-    return int(f) * int(h) * int(w)

@@ -351,6 +351,51 @@ def test_sd35_joint_block_one_image_one_text_token_uniform():
     assert torch.allclose(oh, h2, atol=1e-10) and torch.allclose(oc_, c2, atol=1e-10)
 
 
+def test_sd35_forward_without_blocks_is_patch_embed_then_output():
+    """forward() with no blocks = PatchEmbed (a library Conv2d plus the pinned table
+    crop), AdaLayerNormContinuous (scale first, sd35_batch.py:379-393), proj_out and the
+    unpatchify index map (element-wise): output channel c of pixel (2r + i, 2q + j) is
+    feature (i * 2 + j) * C + c of token r * W' + q; the text only enters through blocks."""
+    cfg, p = _tiny_sd35()
+    ocfg = dict(dim=128, pos_max=384, base_size=64, patch=2, layers=0, eps=1e-6, out_ch=16, heads=2,
+                dual_layers=())
+    lat = torch.randn(16, 6, 10, generator=g(29), dtype=D64)
+    text = torch.randn(3, 32, generator=g(30), dtype=D64)
+    pooled = torch.randn(24, generator=g(31), dtype=D64)
+    table = osd.pos_embed_table(128, max_size=384, base_size=64).double()
+    out = osd.forward(p, ocfg, lat, 250.0, text, pooled, table=table)
+    conv = F.conv2d(lat[None], p["pos_embed.proj.weight"], p["pos_embed.proj.bias"], stride=2)[0]
+    hid = conv.flatten(1).t()  # [3*5, D], token order row-major over the patch grid
+    top, left = (384 - 3) // 2, (384 - 5) // 2
+    hid = hid + torch.stack([table[(top + r) * 384 + left + q] for r in range(3) for q in range(5)])
+    temb = osd.time_text_embed(p, torch.tensor([250.0]), pooled[None])[0]
+    scale, shift = _lin(p, "norm_out.linear", F.silu(temb)).reshape(2, -1).unbind(0)
+    y = _lin(p, "proj_out", F.layer_norm(hid, (128,), eps=1e-6) * (1 + scale) + shift)
+    for c, hh, ww in ((0, 0, 0), (5, 3, 4), (15, 5, 9), (7, 2, 7), (11, 4, 1)):
+        tok = (hh // 2) * 5 + ww // 2
+        feat = ((hh % 2) * 2 + ww % 2) * 16 + c
+        assert abs(float(out[c, hh, ww]) - float(y[tok, feat])) < 1e-10
+    other = osd.forward(p, ocfg, lat, 250.0, torch.zeros_like(text), pooled, table=table)
+    assert torch.equal(out, other)
+    assert all(torch.equal(a, b) for a, b in zip(
+        osd.forward_packed(p, ocfg, [lat, lat[:, :4, :6]], [250.0, 10.0], [text, text[:2]], [pooled, -pooled]),
+        [out, osd.forward(p, ocfg, lat[:, :4, :6], 10.0, text[:2], -pooled, table=table)]))
+
+
+def test_planted_unpatchify_transpose_is_caught(monkeypatch):
+    """An SD3.5 output map with the patch-internal row and column swapped fails the
+    element-wise unpatchify check."""
+    orig = osd.forward
+
+    def wrong(p, cfg, latent, t, text, pooled, attn=oc.sdpa, table=None):
+        out = orig(p, cfg, latent, t, text, pooled, attn, table)
+        c, h, w = out.shape
+        return out.reshape(c, h // 2, 2, w // 2, 2).transpose(2, 4).reshape(c, h, w)
+    _planted(monkeypatch, osd, "forward", wrong)
+    with pytest.raises(AssertionError):
+        test_sd35_forward_without_blocks_is_patch_embed_then_output()
+
+
 # ------------------------------------------------------------ planted mistakes
 def _planted(monkeypatch, module, name, wrong):
     monkeypatch.setattr(module, name, wrong)

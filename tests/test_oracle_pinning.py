@@ -55,6 +55,7 @@ def test_sdpa_matches_library_and_brute_force():
     v = torch.randn(2, 9, 8, generator=g(7), dtype=D64)
     ref = F.scaled_dot_product_attention(q, k, v)
     assert torch.allclose(oc.sdpa(q, k, v, chunk=2), ref, atol=1e-12)
+    assert torch.allclose(oc.sdpa_fast(q, k, v), ref, atol=1e-12)
     out, lse = oc.sdpa_lse(q, k, v)
     # brute force for one query
     s = [sum(float(q[1, 3, d]) * float(k[1, j, d]) for d in range(16)) / 4.0 for j in range(9)]

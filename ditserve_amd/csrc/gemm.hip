@@ -21,6 +21,7 @@
 // computed the same way whatever M is and wherever its row sits: packed and
 // per-request projections agree bitwise.
 #include "ditk_common.h"
+#include "gemm_l4_clobbers.h"
 
 namespace {
 
@@ -379,6 +380,191 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
   }
 }
 
+// Large tiles on one wave per SIMD (every epilogue but fp32, K % 64 == 0): the
+// 256 x 256 workgroup tile as four 128 x 128 wave tiles, 256 accumulators per
+// wave in the AGPRs.  The k loop and the bf16 staging are generated assembly
+// (gen_gemm.py -> gemm_l4_body.inc: 64-k stages through two 64 KiB LDS buffers
+// filled by direct DMA, the next chunk's fragments read under the current
+// MFMAs); this C++ part computes the per-lane addresses and runs the
+// same epilogue arithmetic as gemm_kernel on the staged rows.  Same MFMA
+// (16x16x32, W rows as the A operand), same k order, same bias add and rounding:
+// bitwise equal to gemm_kernel.
+constexpr int L4_STG_ROW = 272;                       // staging row bytes (128 bf16 + 16)
+constexpr int L4_LDS_BYTES = 4 * 128 * L4_STG_ROW;    // staging; the 128 KiB of stages fit inside
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
+    const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
+    const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
+    const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
+    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
+  constexpr int GBM = 256, GBN = 256, WTM = 128, WTN = 128;
+  __shared__ u32x4_t lds[L4_LDS_BYTES / 16];
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int L = (b & 7) * (nb >> 3) + (b >> 3);
+  if (L >= tiles_m * tiles_n) return;
+  const int group = L / (group_m * tiles_n);
+  const int first_m = group * group_m;
+  const int gm = min(group_m, tiles_m - first_m);
+  const int pid = L % (group_m * tiles_n);
+  const int mt = first_m + pid % gm, nt = pid / gm;
+  const int m0 = mt * GBM, n0 = nt * GBN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ql = lane & 15, g = lane >> 4;
+  const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int a_row0 = (wave_u & 1) * WTM, w_row0 = (wave_u >> 1) * WTN;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&lds[0];
+  // fragment reads of 32-k chunk c: row ql of a 16-row fragment, 16-byte unit
+  // 4 c + g of its 64 k, stored at unit (4 c + g) ^ ((row >> 1) & 7) of the
+  // 128-byte LDS row (as gemm_kernel's 64-k stages)
+  uint32_t rdx[2][2], rdw[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const uint32_t lane_part = (uint32_t)(ql * 128 + (((c * 4 + g) ^ ((ql >> 1) & 7)) * 16));
+      rdx[s][c] = lds0 + s * 65536 + a_row0 * 128 + lane_part;
+      rdw[s][c] = lds0 + s * 65536 + 32768 + w_row0 * 128 + lane_part;
+    }
+  // DMA instruction d of this wave fills rows 8 (4 d + wave) .. +7 (1 KiB):
+  // lane l -> row l / 8, LDS unit l % 8 <- k unit (l % 8) ^ ((row >> 1) & 7)
+  uint32_t aoff[8], woff[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const int row = (d * 4 + wave_u) * 8 + lane / 8;
+    const int usw = ((lane & 7) ^ ((row >> 1) & 7)) * 16;
+    aoff[d] = (uint32_t)((int64_t)min(row, M - 1 - m0) * lda * 2 + usw);
+    woff[d] = (uint32_t)((int64_t)min(row, N - 1 - n0) * ldw * 2 + usw);
+  }
+  const uint32_t stg = lds0 + wave_u * (WTM * L4_STG_ROW) + ql * L4_STG_ROW + g * 8;
+  float bv[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f32x4_t x = bias != nullptr
+                          ? *reinterpret_cast<const f32x4_t*>(bias + min(n0 + w_row0 + i * 16 + 4 * g, N - 4))
+                          : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[i * 4 + e] = x[e];
+  }
+  auto su = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+  const uint64_t abase = (uint64_t)(uintptr_t)(A + (int64_t)m0 * lda);
+  const uint64_t wbase = (uint64_t)(uintptr_t)(W + (int64_t)n0 * ldw);
+  asm volatile(
+#include "gemm_l4_body.inc"
+      :
+      : [a_lo] "s"(su((uint32_t)abase)), [a_hi] "s"(su((uint32_t)(abase >> 32))),
+        [w_lo] "s"(su((uint32_t)wbase)), [w_hi] "s"(su((uint32_t)(wbase >> 32))), [nk] "s"(su(K / 64)),
+        [lds] "s"(su(lds0)), [wave1k] "s"(su(wave_u * 1024u)), [rdx00] "v"(rdx[0][0]), [rdx01] "v"(rdx[0][1]),
+        [rdx10] "v"(rdx[1][0]), [rdx11] "v"(rdx[1][1]), [rdw00] "v"(rdw[0][0]), [rdw01] "v"(rdw[0][1]),
+        [rdw10] "v"(rdw[1][0]), [rdw11] "v"(rdw[1][1]), [aoff0] "v"(aoff[0]), [aoff1] "v"(aoff[1]),
+        [aoff2] "v"(aoff[2]), [aoff3] "v"(aoff[3]), [aoff4] "v"(aoff[4]), [aoff5] "v"(aoff[5]),
+        [aoff6] "v"(aoff[6]), [aoff7] "v"(aoff[7]), [woff0] "v"(woff[0]), [woff1] "v"(woff[1]),
+        [woff2] "v"(woff[2]), [woff3] "v"(woff[3]), [woff4] "v"(woff[4]), [woff5] "v"(woff[5]),
+        [woff6] "v"(woff[6]), [woff7] "v"(woff[7]), [stg] "v"(stg), [b0] "v"(bv[0]),
+        [b1] "v"(bv[1]), [b2] "v"(bv[2]), [b3] "v"(bv[3]), [b4] "v"(bv[4]), [b5] "v"(bv[5]), [b6] "v"(bv[6]),
+        [b7] "v"(bv[7]), [b8] "v"(bv[8]), [b9] "v"(bv[9]), [b10] "v"(bv[10]), [b11] "v"(bv[11]),
+        [b12] "v"(bv[12]), [b13] "v"(bv[13]), [b14] "v"(bv[14]), [b15] "v"(bv[15]), [b16] "v"(bv[16]),
+        [b17] "v"(bv[17]), [b18] "v"(bv[18]), [b19] "v"(bv[19]), [b20] "v"(bv[20]), [b21] "v"(bv[21]),
+        [b22] "v"(bv[22]), [b23] "v"(bv[23]), [b24] "v"(bv[24]), [b25] "v"(bv[25]), [b26] "v"(bv[26]),
+        [b27] "v"(bv[27]), [b28] "v"(bv[28]), [b29] "v"(bv[29]), [b30] "v"(bv[30]), [b31] "v"(bv[31])
+      : DITK_GEMM_L4_CLOBBERS "scc", "memory");
+
+  // epilogue on this wave's staged rows (the wave wrote them and waited for them)
+  constexpr int CPR = WTN / 8;        // 16-byte units per row
+  constexpr int RPP = 64 / CPR;       // rows per pass
+  constexpr int NPASS = WTM / RPP;
+  constexpr bool HAS_RES = EPI == EPI_GATE_RES || EPI == EPI_RES;
+  const int c8 = lane % CPR;
+  const int n = n0 + w_row0 + c8 * 8;
+  const int mrow = m0 + a_row0 + lane / CPR;
+  if (n >= N) return;
+  const char* stage = reinterpret_cast<const char*>(lds) + wave_u * (WTM * L4_STG_ROW);
+  int seg_lo = 0;
+  bool one_seg = true;
+  f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_GATE_RES) {
+    seg_lo = find_segment(cu, nseg, m0 + a_row0);
+    one_seg = seg_lo == find_segment(cu, nseg, min(m0 + a_row0 + WTM, M) - 1);
+    if (one_seg) {
+      const float* gp = gate + (int64_t)seg_lo * gate_stride + n;
+      g0 = *reinterpret_cast<const f32x4_t*>(gp);
+      g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
+    }
+  }
+  constexpr int RB = HAS_RES ? 8 : 1;  // residual rows loaded ahead, per batch of passes
+#pragma unroll
+  for (int r0 = 0; r0 < NPASS; r0 += RB) {
+    u32x4_t res[RB];
+    if (HAS_RES) {
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const int m = mrow + (r0 + q) * RPP;
+        res[q] = m < M ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int r = r0 + q;
+      const int t = r * RPP + lane / CPR;
+      const int m = mrow + r * RPP;
+      if (m >= M) continue;
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + t * L4_STG_ROW + c8 * 16);
+      if (EPI != EPI_BIAS) {
+        float x[8];
+        unpack8(v, x);
+        if (EPI == EPI_GELU) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = gelu_tanh_f(x[e]);
+        } else if (EPI == EPI_SILU) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = silu_f(x[e]);
+        } else {
+          float rv[8];
+          unpack8(res[HAS_RES ? q : 0], rv);
+          if (EPI == EPI_GATE_RES) {
+            f32x4_t h0 = g0, h1 = g1;
+            if (!one_seg) {
+              const float* gp = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+              h0 = *reinterpret_cast<const f32x4_t*>(gp);
+              h1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              x[e] = fmaf(x[e], h0[e], rv[e]);
+              x[e + 4] = fmaf(x[e + 4], h1[e], rv[e + 4]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = rv[e] + x[e];
+          }
+        }
+        v = pack8(x);
+      }
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n));
+    }
+  }
+}
+
+template <int EPI>
+int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+              int M, int N, int K, const void* R, int64_t ldr, const float* gate, int64_t gate_stride,
+              const int32_t* cu, int nseg, hipStream_t stream) {
+  const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+  const int64_t nblocks = ((int64_t)tiles_m * tiles_n + 7) / 8 * 8;
+  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
+  gemm_kernel_l4<EPI><<<(unsigned)nblocks, 256, 0, stream>>>(
+      (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
+      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
+  return ditk_check_launch("ditk_gemm");
+}
+
+// The one-wave-per-SIMD kernel where it measured faster than gemm_kernel's large
+// tiles (same box, Wan2.1 block shapes at M = 65520): N >= 3072 or K >= 4096
+// (qkv -3.4%, ffn-up -2.9%, ffn-down -4.7%, N = 3072 SiLU -3.3%).  At N = K = 1536
+// its per-tile prologue and epilogue weigh more and it was 6-8% slower.  The
+// choice changes no result.
+bool use_l4(int N, int K) { return K % 64 == 0 && (N >= 3072 || K >= 4096); }
+
 template <int EPI, int BK, int T>
 int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
                 int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
@@ -409,6 +595,8 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   const int64_t large_tiles = (int64_t)((M + L::GBM - 1) / L::GBM) * ((N + L::GBN - 1) / L::GBN);
   if (large_tiles < kSmallBelow)
     return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  if (EPI != EPI_F32 && use_l4(N, K))
+    return launch_l4<EPI>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }
 

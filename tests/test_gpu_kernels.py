@@ -76,14 +76,16 @@ def test_gemm_rows_independent_of_packing():
     assert torch.equal(full[313:777], part)
 
 
-@pytest.mark.parametrize("epi", ["bias", "gelu", "f32", "gate_res"])
-@pytest.mark.parametrize("K", [1536, 96])
-def test_gemm_tile_configs_agree(epi, K):
+@pytest.mark.parametrize("epi", ["bias", "gelu", "f32", "gate_res", "res", "silu"])
+@pytest.mark.parametrize("K,N", [(1536, 3072), (96, 2048), (4160, 1024)])
+def test_gemm_tile_configs_agree(epi, K, N):
     """Large M runs 256x256 workgroup tiles, a few hundred rows the 64x128 ones;
-    both use the same MFMA, k order and epilogue arithmetic, so rows computed
-    in either are bitwise equal (K = 96 takes the 32-k stage path of both)."""
+    all use the same MFMA, k order and epilogue arithmetic, so rows computed in
+    either are bitwise equal.  N = 3072 and K = 4160 take the one-wave-per-SIMD
+    kernel with the generated k loop (the fp32 epilogue and K = 96, an odd number
+    of 32-k stages, the 8-wave one)."""
     ops = _ops()
-    M, N = 8192, 2048  # 32 x 8 large tiles: the large configuration
+    M = 8192  # 32 x 12, 32 x 8 or 32 x 4 large tiles: the large configuration
     a = randn((M, K), 40).to(DEV, torch.bfloat16)
     w = randn((N, K), 41, 0.02).to(DEV, torch.bfloat16)
     b = randn((N,), 42).to(DEV)
@@ -91,10 +93,14 @@ def test_gemm_tile_configs_agree(epi, K):
     if epi == "gate_res":
         kw = dict(residual=randn((M, N), 43).to(DEV, torch.bfloat16), gate=randn((2, N), 44).to(DEV),
                   segments=_seg([0, 5000, M]))
+    elif epi == "res":
+        kw = dict(residual=randn((M, N), 43).to(DEV, torch.bfloat16))
     full = ops.linear(a, w, b, epi, **kw)
-    lo, hi = 4700, 5333  # 633 rows across the segment boundary: 3 x 8 large tiles, so small ones run
+    lo, hi = 4700, 5333  # 633 rows across the segment boundary: at most 3 x 12 large tiles, so small ones run
     if epi == "gate_res":
         kw = dict(residual=kw["residual"][lo:hi].contiguous(), gate=kw["gate"], segments=_seg([0, 5000 - lo, hi - lo]))
+    elif epi == "res":
+        kw = dict(residual=kw["residual"][lo:hi].contiguous())
     part = ops.linear(a[lo:hi].contiguous(), w, b, epi, **kw)
     assert torch.equal(full[lo:hi], part)
 

@@ -517,38 +517,37 @@ def prologue(g):
     g(f"s_sub_u32 {s_(S_NKT1)}, %[nkt], 1")
     g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
     g(f"s_mov_b32 {s_(S_THR)}, 0x43800000")
-    # Q fragments straight into AGPRs
+    # Q fragments straight into AGPRs, then the DMAs of K(0) (K stage 0), K(1)
+    # (K stage 1; K(0) again when there is one tile) and Vt(0) (Vt stage 0), all
+    # before the first wait so that their latencies overlap
     for qb in range(2):
         for c in range(8):
             g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, %[qoff{qb}], %[qbase] offset:{c * 32}")
-    # O = 0, l = 0
+    for i in range(4):
+        g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
+    g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
+    g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
+    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
+    kdma_block(g, 0)
+    g(f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
+    g(f"s_cselect_b32 {s_(S_T0)}, 0, %[ktile]")
+    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, {s_(S_T0)}")
+    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
+    clamp_koff(g, f"s_cmp_le_u32 {s_(S_NKT1)}, 1")
+    kdma_block(g, 1)
+    vdma_block(g, 0)
+    g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
+    g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
+    # O = 0, l = 0 while the loads fly
     for i in range(128):
         g(f"v_accvgpr_write_b32 {ar(O_A + i)}, 0")
     for qb in range(2):
         g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
         g(f"v_mov_b32 {vr(RS1 + qb)}, 0")
-    for i in range(4):
-        g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
-    # K(0) into K stage 0 (clamped when it is the last tile)
-    g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
-    g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
-    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
-    kdma_block(g, 0)
-    g("s_waitcnt vmcnt(0)")
+    # Q and K(0) landed (the 8 DMAs of K(1) and Vt(0) may still fly), K(0) published
+    g("s_waitcnt vmcnt(8)")
     g("s_barrier")
-    # K(1) into K stage 1 when nkt > 1 (clamped when last); Vt(0) into Vt stage 0
-    no_k1 = g.new_label("nok1")
-    g(f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
-    g(f"s_cbranch_scc1 {no_k1}")
-    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[ktile]")
-    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
-    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 1")
-    kdma_block(g, 1)
-    g.label(no_k1)
-    vdma_block(g, 0)
-    g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
-    g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
     # S(0) = K(0) Q^T into set A
     g.lds = []
     for c in range(2):

@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
       g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
     }
   }
-  constexpr int RB = HAS_RES ? 8 : 1;  // residual rows loaded ahead, per batch of passes
+  constexpr int RB = HAS_RES ? NPASS : 1;  // every residual row loaded before the passes
 #pragma unroll
   for (int r0 = 0; r0 < NPASS; r0 += RB) {
     u32x4_t res[RB];

@@ -389,16 +389,42 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
 // same epilogue arithmetic as gemm_kernel on the staged rows.  Same MFMA
 // (16x16x32, W rows as the A operand), same k order, same bias add and rounding:
 // bitwise equal to gemm_kernel.
-constexpr int L4_STG_ROW = 272;                       // staging row bytes (128 bf16 + 16)
-constexpr int L4_LDS_BYTES = 4 * 128 * L4_STG_ROW;    // staging; the 128 KiB of stages fit inside
-template <int EPI>
+// FI feature fragments of 16 per wave tile: 8 (128 x 128 wave tiles, 256 x 256
+// workgroup tiles, gemm_l4_body.inc) or 6 (128 x 96, 256 x 192,
+// gemm_l4w96_body.inc: for shapes whose 256-wide tiles would leave CUs idle in
+// the last round).
+template <int FI>
+struct L4 {
+  static constexpr int WTM = 128, WTN = 16 * FI, GBM = 256, GBN = 2 * WTN;
+  static constexpr int BUF = (GBM + GBN) * 128;            // one 64-k stage: A rows, then W rows
+  static constexpr int STG_ROW = 2 * WTN + 16;             // staging row bytes
+  static constexpr int LDS_BYTES = 2 * BUF > 4 * WTM * STG_ROW ? 2 * BUF : 4 * WTM * STG_ROW;
+};
+#define DITK_L4_OPERANDS                                                                                        \
+  [a_lo] "s"(su((uint32_t)abase)), [a_hi] "s"(su((uint32_t)(abase >> 32))), [w_lo] "s"(su((uint32_t)wbase)),   \
+      [w_hi] "s"(su((uint32_t)(wbase >> 32))), [nk] "s"(su(K / 64)), [lds] "s"(su(lds0)),                       \
+      [wave1k] "s"(su(wave_u * 1024u)), [rdx00] "v"(rdx[0][0]), [rdx01] "v"(rdx[0][1]), [rdx10] "v"(rdx[1][0]), \
+      [rdx11] "v"(rdx[1][1]), [rdw00] "v"(rdw[0][0]), [rdw01] "v"(rdw[0][1]), [rdw10] "v"(rdw[1][0]),           \
+      [rdw11] "v"(rdw[1][1]), [aoff0] "v"(aoff[0]), [aoff1] "v"(aoff[1]), [aoff2] "v"(aoff[2]),                 \
+      [aoff3] "v"(aoff[3]), [aoff4] "v"(aoff[4]), [aoff5] "v"(aoff[5]), [aoff6] "v"(aoff[6]),                   \
+      [aoff7] "v"(aoff[7]), [woff0] "v"(woff[0]), [woff1] "v"(woff[1]), [woff2] "v"(woff[2]),                   \
+      [woff3] "v"(woff[3]), [woff4] "v"(woff[4]), [woff5] "v"(woff[5]), [woff6] "v"(woff[6]),                   \
+      [woff7] "v"(woff[7]), [stg] "v"(stg), [b0] "v"(bv[0]), [b1] "v"(bv[1]), [b2] "v"(bv[2]), [b3] "v"(bv[3]),  \
+      [b4] "v"(bv[4]), [b5] "v"(bv[5]), [b6] "v"(bv[6]), [b7] "v"(bv[7]), [b8] "v"(bv[8]), [b9] "v"(bv[9]),      \
+      [b10] "v"(bv[10]), [b11] "v"(bv[11]), [b12] "v"(bv[12]), [b13] "v"(bv[13]), [b14] "v"(bv[14]),            \
+      [b15] "v"(bv[15]), [b16] "v"(bv[16]), [b17] "v"(bv[17]), [b18] "v"(bv[18]), [b19] "v"(bv[19]),            \
+      [b20] "v"(bv[20]), [b21] "v"(bv[21]), [b22] "v"(bv[22]), [b23] "v"(bv[23]), [b24] "v"(bv[24]),            \
+      [b25] "v"(bv[25]), [b26] "v"(bv[26]), [b27] "v"(bv[27]), [b28] "v"(bv[28]), [b29] "v"(bv[29]),            \
+      [b30] "v"(bv[30]), [b31] "v"(bv[31])
+template <int EPI, int FI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
-  constexpr int GBM = 256, GBN = 256, WTM = 128, WTN = 128;
-  __shared__ u32x4_t lds[L4_LDS_BYTES / 16];
+  using G = L4<FI>;
+  constexpr int GBM = G::GBM, GBN = G::GBN, WTM = G::WTM, WTN = G::WTN, STG_ROW = G::STG_ROW;
+  __shared__ u32x4_t lds[G::LDS_BYTES / 16];
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (b & 7) * (nb >> 3) + (b >> 3);
   if (L >= tiles_m * tiles_n) return;
@@ -423,8 +449,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const uint32_t lane_part = (uint32_t)(ql * 128 + (((c * 4 + g) ^ ((ql >> 1) & 7)) * 16));
-      rdx[s][c] = lds0 + s * 65536 + a_row0 * 128 + lane_part;
-      rdw[s][c] = lds0 + s * 65536 + 32768 + w_row0 * 128 + lane_part;
+      rdx[s][c] = lds0 + s * G::BUF + a_row0 * 128 + lane_part;
+      rdw[s][c] = lds0 + s * G::BUF + GBM * 128 + w_row0 * 128 + lane_part;
     }
   // DMA instruction d of this wave fills rows 8 (4 d + wave) .. +7 (1 KiB):
   // lane l -> row l / 8, LDS unit l % 8 <- k unit (l % 8) ^ ((row >> 1) & 7)
@@ -434,13 +460,13 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
     const int row = (d * 4 + wave_u) * 8 + lane / 8;
     const int usw = ((lane & 7) ^ ((row >> 1) & 7)) * 16;
     aoff[d] = (uint32_t)((int64_t)min(row, M - 1 - m0) * lda * 2 + usw);
-    woff[d] = (uint32_t)((int64_t)min(row, N - 1 - n0) * ldw * 2 + usw);
+    woff[d] = d < FI ? (uint32_t)((int64_t)min(row, N - 1 - n0) * ldw * 2 + usw) : 0u;
   }
-  const uint32_t stg = lds0 + wave_u * (WTM * L4_STG_ROW) + ql * L4_STG_ROW + g * 8;
+  const uint32_t stg = lds0 + wave_u * (WTM * STG_ROW) + ql * STG_ROW + g * 8;
   float bv[32];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const f32x4_t x = bias != nullptr
+    const f32x4_t x = bias != nullptr && i < FI
                           ? *reinterpret_cast<const f32x4_t*>(bias + min(n0 + w_row0 + i * 16 + 4 * g, N - 4))
                           : f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -449,36 +475,25 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
   auto su = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
   const uint64_t abase = (uint64_t)(uintptr_t)(A + (int64_t)m0 * lda);
   const uint64_t wbase = (uint64_t)(uintptr_t)(W + (int64_t)n0 * ldw);
-  asm volatile(
+  if constexpr (FI == 8)
+    asm volatile(
 #include "gemm_l4_body.inc"
-      :
-      : [a_lo] "s"(su((uint32_t)abase)), [a_hi] "s"(su((uint32_t)(abase >> 32))),
-        [w_lo] "s"(su((uint32_t)wbase)), [w_hi] "s"(su((uint32_t)(wbase >> 32))), [nk] "s"(su(K / 64)),
-        [lds] "s"(su(lds0)), [wave1k] "s"(su(wave_u * 1024u)), [rdx00] "v"(rdx[0][0]), [rdx01] "v"(rdx[0][1]),
-        [rdx10] "v"(rdx[1][0]), [rdx11] "v"(rdx[1][1]), [rdw00] "v"(rdw[0][0]), [rdw01] "v"(rdw[0][1]),
-        [rdw10] "v"(rdw[1][0]), [rdw11] "v"(rdw[1][1]), [aoff0] "v"(aoff[0]), [aoff1] "v"(aoff[1]),
-        [aoff2] "v"(aoff[2]), [aoff3] "v"(aoff[3]), [aoff4] "v"(aoff[4]), [aoff5] "v"(aoff[5]),
-        [aoff6] "v"(aoff[6]), [aoff7] "v"(aoff[7]), [woff0] "v"(woff[0]), [woff1] "v"(woff[1]),
-        [woff2] "v"(woff[2]), [woff3] "v"(woff[3]), [woff4] "v"(woff[4]), [woff5] "v"(woff[5]),
-        [woff6] "v"(woff[6]), [woff7] "v"(woff[7]), [stg] "v"(stg), [b0] "v"(bv[0]),
-        [b1] "v"(bv[1]), [b2] "v"(bv[2]), [b3] "v"(bv[3]), [b4] "v"(bv[4]), [b5] "v"(bv[5]), [b6] "v"(bv[6]),
-        [b7] "v"(bv[7]), [b8] "v"(bv[8]), [b9] "v"(bv[9]), [b10] "v"(bv[10]), [b11] "v"(bv[11]),
-        [b12] "v"(bv[12]), [b13] "v"(bv[13]), [b14] "v"(bv[14]), [b15] "v"(bv[15]), [b16] "v"(bv[16]),
-        [b17] "v"(bv[17]), [b18] "v"(bv[18]), [b19] "v"(bv[19]), [b20] "v"(bv[20]), [b21] "v"(bv[21]),
-        [b22] "v"(bv[22]), [b23] "v"(bv[23]), [b24] "v"(bv[24]), [b25] "v"(bv[25]), [b26] "v"(bv[26]),
-        [b27] "v"(bv[27]), [b28] "v"(bv[28]), [b29] "v"(bv[29]), [b30] "v"(bv[30]), [b31] "v"(bv[31])
-      : DITK_GEMM_L4_CLOBBERS "scc", "memory");
+        : : DITK_L4_OPERANDS : DITK_GEMM_L4_CLOBBERS "scc", "memory");
+  else
+    asm volatile(
+#include "gemm_l4w96_body.inc"
+        : : DITK_L4_OPERANDS : DITK_GEMM_L4_CLOBBERS "scc", "memory");
 
   // epilogue on this wave's staged rows (the wave wrote them and waited for them)
-  constexpr int CPR = WTN / 8;        // 16-byte units per row
-  constexpr int RPP = 64 / CPR;       // rows per pass
-  constexpr int NPASS = WTM / RPP;
+  constexpr int CPR = WTN / 8;                    // 16-byte units per row (16 or 12)
+  constexpr int RPP = 64 / CPR;                   // rows per pass (4 or 5; lanes past RPP * CPR idle)
+  constexpr int NPASS = (WTM + RPP - 1) / RPP;
   constexpr bool HAS_RES = EPI == EPI_GATE_RES || EPI == EPI_RES;
   const int c8 = lane % CPR;
   const int n = n0 + w_row0 + c8 * 8;
   const int mrow = m0 + a_row0 + lane / CPR;
-  if (n >= N) return;
-  const char* stage = reinterpret_cast<const char*>(lds) + wave_u * (WTM * L4_STG_ROW);
+  if (n >= N || lane >= RPP * CPR) return;
+  const char* stage = reinterpret_cast<const char*>(lds) + wave_u * (WTM * STG_ROW);
   int seg_lo = 0;
   bool one_seg = true;
   f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
@@ -499,7 +514,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
         const int m = mrow + (r0 + q) * RPP;
-        res[q] = m < M ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
+        const bool in = m < M && (r0 + q) * RPP + lane / CPR < WTM;
+        res[q] = in ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -507,8 +523,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
       const int r = r0 + q;
       const int t = r * RPP + lane / CPR;
       const int m = mrow + r * RPP;
-      if (m >= M) continue;
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + t * L4_STG_ROW + c8 * 16);
+      if (m >= M || t >= WTM) continue;
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + t * STG_ROW + c8 * 16);
       if (EPI != EPI_BIAS) {
         float x[8];
         unpack8(v, x);
@@ -545,14 +561,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
   }
 }
 
-template <int EPI>
+template <int EPI, int FI>
 int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
               int M, int N, int K, const void* R, int64_t ldr, const float* gate, int64_t gate_stride,
               const int32_t* cu, int nseg, hipStream_t stream) {
-  const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+  constexpr int GBN = L4<FI>::GBN;
+  const int tiles_m = (M + 255) / 256, tiles_n = (N + GBN - 1) / GBN;
   const int64_t nblocks = ((int64_t)tiles_m * tiles_n + 7) / 8 * 8;
   DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
-  gemm_kernel_l4<EPI><<<(unsigned)nblocks, 256, 0, stream>>>(
+  gemm_kernel_l4<EPI, FI><<<(unsigned)nblocks, 256, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
       gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
   return ditk_check_launch("ditk_gemm");
@@ -564,6 +581,28 @@ int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
 // its per-tile prologue and epilogue weigh more and it was 6-8% slower.  The
 // choice changes no result.
 bool use_l4(int N, int K) { return K % 64 == 0 && (N >= 3072 || K >= 4096); }
+
+// 256 x 192 tiles when they fill the GPU's CUs in fewer tile-rounds, weighted
+// by tile width, than 256 x 256 ones (the two take the same time per unit of
+// width): e.g. M = 8192 and N = 1536 is 256 tiles = one round instead of 192 =
+// one round with a quarter of the CUs idle; N = 4608 is 768 tiles = 3 rounds
+// instead of 576 = 2.25 (so 3).  Ties keep the 256-wide tiles (fewer bytes
+// moved per FLOP).
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+bool use_w192(int M, int N) {
+  const int64_t tm = (M + 255) / 256, ncu = cu_count();
+  const int64_t r256 = (tm * ((N + 255) / 256) + ncu - 1) / ncu, r192 = (tm * ((N + 191) / 192) + ncu - 1) / ncu;
+  return r192 * 192 < r256 * 256;
+}
 
 template <int EPI, int BK, int T>
 int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
@@ -595,8 +634,10 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   const int64_t large_tiles = (int64_t)((M + L::GBM - 1) / L::GBM) * ((N + L::GBN - 1) / L::GBN);
   if (large_tiles < kSmallBelow)
     return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  if (EPI != EPI_F32 && K % 64 == 0 && use_w192(M, N))
+    return launch_l4<EPI, 6>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   if (EPI != EPI_F32 && use_l4(N, K))
-    return launch_l4<EPI>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+    return launch_l4<EPI, 8>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }
 

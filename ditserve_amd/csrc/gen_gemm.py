@@ -32,19 +32,35 @@ Every output element accumulates the same MFMAs over the same k order as the
 C++ kernels (gemm_kernel), and the bias add and rounding are the same
 instructions, so the results are bitwise theirs.
 
-Usage: python gen_gemm.py [out.inc]  (default gemm_l4_body.inc beside this file;
-gemm_l4_clobbers.h is written beside the output)
+Two wave-tile widths are generated: 128 features (gemm_l4_body.inc, workgroup
+tile 256 x 256) and 96 (gemm_l4w96_body.inc, 256 x 192, 192 accumulators) for
+the shapes where 192-wide tiles fill the 256 CUs in fewer rounds.
+
+Usage: python gen_gemm.py [dir/any]  (writes gemm_l4_body.inc, gemm_l4w96_body.inc
+and gemm_l4_clobbers.h into that directory, default beside this file)
 """
 import os
 import sys
 
-BUF = 64 * 1024         # bytes per stage buffer: A rows [0, 32 KiB), W rows [32, 64 KiB)
-WOFF = 32 * 1024
+FJ = 8                  # token fragments per wave tile (128 tokens)
+
+
+def configure(fi):  # noqa: D401
+    """fi feature fragments per wave tile: 8 (wave tile 128 x 128, workgroup tile
+    256 x 256) or 6 (128 x 96, workgroup 256 x 192)."""
+    global FI, BUF, WOFF, STG_ROW, ND, DMA_SLOTS
+    FI = fi
+    BUF = (256 + 32 * fi) * 128        # stage buffer: A rows (32 KiB), then W rows
+    WOFF = 32 * 1024
+    STG_ROW = 32 * fi + 16             # staging row: 16 fi bf16 features + 16 bytes
+    ND = 8 + fi                        # DMA instructions per wave and stage (A groups, then W)
+    step = fi * FJ // ND                # chunk-1 MFMA slots of the stage's DMAs, evenly spread
+    DMA_SLOTS = [step * k + 2 for k in range(ND)]
+    assert DMA_SLOTS[-1] < fi * FJ and 2 * (fi + FJ) <= fi * FJ
+
+
+configure(8)
 ROW = 128               # bytes per LDS row (64 k of bf16)
-STG_ROW = 272           # bytes per staging row (256 + 16)
-FI = FJ = 8             # W / token fragments per wave tile
-ND = 16                 # DMA instructions per wave and stage (8 A groups, then 8 W groups)
-DMA_SLOTS = [4 * k + 2 for k in range(ND)]   # chunk-1 MFMA slots of the stage's DMAs
 
 S_A, S_W = 40, 42       # s[40:41], s[42:43] DMA bases of the stage being fetched
 S_S, S_NK1, S_SW = 44, 45, 46   # stage index, nk - 1, LDS + 1 KiB wave slice
@@ -222,16 +238,23 @@ def clobbers():
             "#define DITK_GEMM_L4_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
 
 
-def main(argv):
-    here = os.path.dirname(os.path.abspath(__file__))
-    out = argv[1] if len(argv) > 1 else os.path.join(here, "gemm_l4_body.inc")
+def write_body(path, fi):
+    configure(fi)
     lines = generate()
-    with open(out, "w") as f:
-        f.write("// Generated by gen_gemm.py -- the instruction body of gemm_kernel_l4.\n")
+    with open(path, "w") as f:
+        f.write(f"// Generated by gen_gemm.py -- the instruction body of gemm_kernel_l4<FI = {fi}>.\n")
         for line in lines:
             esc = line.replace("\\", "\\\\").replace('"', '\\"')
             f.write(f'"{esc}\\n"\n')
-    with open(os.path.join(os.path.dirname(os.path.abspath(out)), "gemm_l4_clobbers.h"), "w") as f:
+
+
+def main(argv):
+    here = os.path.dirname(os.path.abspath(__file__))
+    out = os.path.dirname(os.path.abspath(argv[1])) if len(argv) > 1 else here
+    write_body(os.path.join(out, "gemm_l4_body.inc"), 8)
+    write_body(os.path.join(out, "gemm_l4w96_body.inc"), 6)
+    configure(8)
+    with open(os.path.join(out, "gemm_l4_clobbers.h"), "w") as f:
         f.write(clobbers())
     return 0
 

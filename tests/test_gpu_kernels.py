@@ -26,7 +26,8 @@ def _seg(cu):
 # --------------------------------------------------------------------------- GEMM
 GEMM_CASES = [(1000, 1536, 1536), (256, 4608, 1536), (77, 64, 1536), (513, 384, 8960), (33, 1536, 64),
               (300, 512, 96),  # K % 64 == 32: the 32-k stage path
-              (4000, 4104, 1536)]  # 16 x 17 = 272 256x256 tiles (the large configuration), ragged M and N
+              (4000, 4104, 1536),  # 16 x 22 256x192 tiles (two rounds, fewer than 16 x 17 256x256), ragged M and N
+              (4000, 4096, 1536)]  # 16 x 16 256x256 tiles (one round; 256x192 would take two), ragged M
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
@@ -77,15 +78,16 @@ def test_gemm_rows_independent_of_packing():
 
 
 @pytest.mark.parametrize("epi", ["bias", "gelu", "f32", "gate_res", "res", "silu"])
-@pytest.mark.parametrize("K,N", [(1536, 3072), (96, 2048), (4160, 1024)])
+@pytest.mark.parametrize("K,N", [(1536, 4096), (1536, 1536), (96, 2048), (4160, 2048), (4160, 1024)])
 def test_gemm_tile_configs_agree(epi, K, N):
-    """Large M runs 256x256 workgroup tiles, a few hundred rows the 64x128 ones;
-    all use the same MFMA, k order and epilogue arithmetic, so rows computed in
-    either are bitwise equal.  N = 3072 and K = 4160 take the one-wave-per-SIMD
-    kernel with the generated k loop (the fp32 epilogue and K = 96, an odd number
-    of 32-k stages, the 8-wave one)."""
+    """Large M runs large workgroup tiles, a few hundred rows the 64x128 ones; all
+    use the same MFMA, k order and epilogue arithmetic, so rows computed in either
+    are bitwise equal.  At M = 8192 on 256 CUs: N = 4096 and (K = 4160, N = 2048)
+    take the one-wave-per-SIMD 256x256 kernel, N = 1536 and (4160, 1024) its
+    256x192 form (fewer tile rounds), K = 96 (an odd number of 32-k stages) and
+    the fp32 epilogue the 8-wave kernel."""
     ops = _ops()
-    M = 8192  # 32 x 12, 32 x 8 or 32 x 4 large tiles: the large configuration
+    M = 8192
     a = randn((M, K), 40).to(DEV, torch.bfloat16)
     w = randn((N, K), 41, 0.02).to(DEV, torch.bfloat16)
     b = randn((N,), 42).to(DEV)
@@ -96,7 +98,7 @@ def test_gemm_tile_configs_agree(epi, K, N):
     elif epi == "res":
         kw = dict(residual=randn((M, N), 43).to(DEV, torch.bfloat16))
     full = ops.linear(a, w, b, epi, **kw)
-    lo, hi = 4700, 5333  # 633 rows across the segment boundary: at most 3 x 12 large tiles, so small ones run
+    lo, hi = 4700, 5333  # 633 rows across the segment boundary: at most 3 x 16 large tiles, so small ones run
     if epi == "gate_res":
         kw = dict(residual=kw["residual"][lo:hi].contiguous(), gate=kw["gate"], segments=_seg([0, 5000 - lo, hi - lo]))
     elif epi == "res":

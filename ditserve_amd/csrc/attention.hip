@@ -46,6 +46,7 @@
 
 #include "ditk_common.h"
 #include "attn_d128_clobbers.h"
+#include "attn_d64_clobbers.h"
 
 namespace {
 
@@ -675,19 +676,34 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
   }
 }
 
-// head_dim 128, 64 queries per wave (two 32-query blocks), one wave per SIMD:
-// four waves and 256 queries per workgroup.  The C++ side locates the work item
-// and computes per-lane addresses; the body is generated assembly
-// (gen_attn_d128.py -> attn_d128_body.inc) with its registers placed by hand:
-// O^T and Q in AGPRs, S^T and P in VGPRs, so that the whole working set (about
-// 460 registers per lane) stays in registers.  Same arithmetic, same order of
-// every sum and the same lazy-rescale rule as flash_fwd_kernel, per score.
-__global__ __launch_bounds__(256, 1) void flash_fwd_d128(
+// head_dim 128 or 64, 64 queries per wave (two 32-query blocks), one wave per
+// SIMD: four waves and 256 queries per workgroup.  The C++ side locates the work
+// item and computes per-lane addresses; the body is generated assembly
+// (gen_attn.py -> attn_d128_body.inc / attn_d64_body.inc) with its registers
+// placed by hand: O^T and Q in AGPRs, S^T and P in VGPRs, so that the whole
+// working set stays in registers.  Same arithmetic, same order of every sum and
+// the same lazy-rescale rule as flash_fwd_kernel, per score.
+#define DITK_ATTN_ASM_OPERANDS                                                                                      \
+  [qbase] "s"(su64(qbase)), [qoff0] "v"(qoff0), [qoff1] "v"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),            \
+      [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
+      [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
+      [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
+      [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),             \
+      [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
+      [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
+      [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
+      [koff0] "v"(koff[0]), [koff1] "v"(koff[1]), [koff2] "v"(koff[2]), [koff3] "v"(koff[3]),                     \
+      [koffl0] "v"(koffl[0]), [koffl1] "v"(koffl[1]), [koffl2] "v"(koffl[2]), [koffl3] "v"(koffl[3]),             \
+      [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
+      [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0), [qrow1] "v"(qrow1)
+template <int HD>
+__global__ __launch_bounds__(256, 1) void flash_fwd_asm(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
     float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
-  constexpr int HD = 128, NW = 4, BM = 256;
+  constexpr int NW = 4, BM = 256;
+  constexpr int ND = HD / 32;  // DMA instructions per wave and operand per tile
   __shared__ u32x4_t Ks[2][BN * HD / 8];
   __shared__ u32x4_t Vs[2][HD * 8];
   const int nb = gridDim.x;
@@ -709,7 +725,7 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
     for (int qb = 0; qb < 2; ++qb) {
       const int qrow = qb ? qrow1 : qrow0;
       if (qrow < q_end) {
-        for (int d = hh * 64; d < hh * 64 + 64; ++d) O[(int64_t)qrow * ldo + (int64_t)head * HD + d] = 0;
+        for (int d = hh * (HD / 2); d < (hh + 1) * (HD / 2); ++d) O[(int64_t)qrow * ldo + (int64_t)head * HD + d] = 0;
         if (lse != nullptr && hh == 0) lse[(int64_t)head * lse_ld + qrow] = -INFINITY;
       }
     }
@@ -733,7 +749,7 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
   // last row) and Vt DMA source offsets, per lane
   const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Ks[0][0];
   const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Vs[0][0];
-  uint32_t kaddr[4], vaddr[4], koff[4], koffl[4], voff[4];
+  uint32_t kaddr[4], vaddr[4], koff[4] = {}, koffl[4] = {}, voff[4] = {};
   const int lrow = lane >> 3;
   const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;
   const int lsw1 = ((lane & 7) ^ (((lane >> 4) + 4) & 7)) * 8;
@@ -741,6 +757,9 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
   for (int i = 0; i < 4; ++i) {
     kaddr[i] = lds_k + (uint32_t)(kr * 8 + ((i * 2 + hh) ^ kg)) * 16;
     vaddr[i] = lds_v + (uint32_t)(l32 * 8 + ((i * 2 + hh) ^ vg)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
     const int g = i * NW + wave_u;
     const int grp = g / (BN / 8), r8 = g % (BN / 8);
     const uint32_t krow = (uint32_t)(r8 * 8 + lrow);
@@ -761,23 +780,15 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_d128(
   auto su = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
   auto su64 = [&](uint64_t x) { return ((uint64_t)su((uint32_t)(x >> 32)) << 32) | su((uint32_t)x); };
   const float sc = __builtin_bit_cast(float, su(__builtin_bit_cast(uint32_t, scale_log2)));
-  asm volatile(
+  if constexpr (HD == 128) {
+    asm volatile(
 #include "attn_d128_body.inc"
-      :
-      : [qbase] "s"(su64(qbase)), [qoff0] "v"(qoff0), [qoff1] "v"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),
-        [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),
-        [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),
-        [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)),
-        [wave1k] "s"(su(wave1k)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)),
-        [obase_lo] "s"(su((uint32_t)obase)), [obase_hi] "s"(su((uint32_t)(obase >> 32))),
-        [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)), [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]),
-        [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]), [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]),
-        [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]), [koff0] "v"(koff[0]), [koff1] "v"(koff[1]),
-        [koff2] "v"(koff[2]), [koff3] "v"(koff[3]), [koffl0] "v"(koffl[0]), [koffl1] "v"(koffl[1]),
-        [koffl2] "v"(koffl[2]), [koffl3] "v"(koffl[3]), [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]),
-        [voff3] "v"(voff[3]), [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0),
-        [qrow1] "v"(qrow1)
-      : DITK_D128_CLOBBERS "vcc", "scc", "memory");
+        : : DITK_ATTN_ASM_OPERANDS : DITK_D128_CLOBBERS "vcc", "scc", "memory");
+  } else {
+    asm volatile(
+#include "attn_d64_body.inc"
+        : : DITK_ATTN_ASM_OPERANDS : DITK_D64_CLOBBERS "vcc", "scc", "memory");
+  }
 }
 
 // V [Tk, ldv] (head h at columns h*HD..) -> Vt [heads][HD][vt_ld], per-segment
@@ -917,7 +928,7 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, true>, kWaves * kQBlocks * 32, kWaves * 64);
   else if (pre)
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, false>, kWaves * kQBlocks * 32, kWaves * 64);
-  else if (head_dim == 128) {
+  else {
     // one wave per SIMD, 64 queries per wave: generated-assembly body
     DITK_REQUIRE((int64_t)Tq * ldq * 2 < (1ll << 32) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
                  "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
@@ -925,13 +936,12 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     int64_t nblocks = (int64_t)tiles_bound * heads;
     nblocks = (nblocks + 7) / 8 * 8;
     DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
-    flash_fwd_d128<<<(unsigned)nblocks, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk,
-                                                        (const bf16_t*)vt, vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld,
-                                                        cu_q, cu_k, nseg, heads, tiles_bound, sl2);
+    auto kern = head_dim == 128 ? flash_fwd_asm<128> : flash_fwd_asm<64>;
+    kern<<<(unsigned)nblocks, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk, (const bf16_t*)vt,
+                                                vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld, cu_q, cu_k, nseg, heads,
+                                                tiles_bound, sl2);
     rc = 0;
   }
-  else
-    rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, false, false>, kWaves * kQBlocks * 32, kWaves * 64);
   if (rc) return rc;
   return ditk_check_launch("ditk_flash_attn_varlen");
 }

@@ -1,10 +1,11 @@
-"""Generate the instruction body of the head_dim-128 varlen flash-attention
-kernel (attention.hip: flash_fwd_d128) as gfx950 assembly.
+"""Generate the instruction body of the varlen flash-attention kernel
+(attention.hip: flash_fwd_asm<HD>) as gfx950 assembly, for head dims 128 and 64.
 
 Why generated assembly: the kernel runs one wave per SIMD with 64 queries per
 wave, which needs about 460 registers per lane.  The compiler cannot place that
 working set (its allocation spills or shuffles AGPR<->VGPR copies), so the
-registers are assigned here by hand:
+registers are assigned here by hand (head dim 128; at head dim 64 the O, Q, K
+and Vt blocks halve and the VGPR map is the same):
 
   VGPR v0..v63     S set A   S^T accumulators [qb][kk] (16 each) of one key tile
   VGPR v64..v127   S set B   (the loop is unrolled by two so that the tile being
@@ -41,22 +42,44 @@ Hazards the hardware does not interlock are covered explicitly: an s_nop before
 VALU reads of MFMA results and before MFMAs read AGPRs written by
 v_accvgpr_write, an s_nop between an M0 write and the DMA that reads it.
 
-Usage: python gen_attn_d128.py [out.inc]  (default attn_d128_body.inc beside this
-file; attn_d128_clobbers.h is written beside the output)
+Usage: python gen_attn.py [dir/any]  (writes attn_d128_body.inc, attn_d128_clobbers.h,
+attn_d64_body.inc and attn_d64_clobbers.h into that directory, default beside
+this file)
 """
 import os
 import sys
 
 # ----------------------------------------------------------------------------
-# register map
+# register map (VGPRs: the same for both head dims)
 S_SET = (0, 64)
 P_SET = (128, 160)
 TMP = 192
 RS0, RS1, NEGM, LRUN = 200, 202, 204, 206
 KOFF, DTMP = 208, 212
-O_A, Q_A, KF_A, VF_A = 0, 128, 192, 216
 VRING = 6        # Vt fragment ring (read four fragments ahead)
-LAST_VGPR, LAST_AGPR = 215, VF_A + 4 * VRING - 1
+LAST_VGPR = 215
+BN = 64
+
+
+def configure(hd):
+    """Head dim 128 or 64: NC 16-wide chunks of the head dim (K fragments per key
+    half), DT 32-row d tiles of O^T, NF Vt fragments per tile (4 key groups x DT),
+    ND DMA instructions per wave and operand per tile; AGPRs: O^T, then Q, the K
+    ring (3 chunks x 2 key halves) and the Vt ring."""
+    global HD, NC, DT, NF, ND, KSTAGE_BYTES, VSTAGE_BYTES, O_A, Q_A, KF_A, VF_A, LAST_AGPR
+    HD = hd
+    NC, DT = hd // 16, hd // 32
+    NF = 4 * DT
+    ND = hd // 32
+    KSTAGE_BYTES = VSTAGE_BYTES = BN * hd * 2
+    O_A = 0
+    Q_A = O_A + 2 * DT * 16
+    KF_A = Q_A + 2 * NC * 4
+    VF_A = KF_A + 3 * 2 * 4
+    LAST_AGPR = VF_A + 4 * VRING - 1
+
+
+configure(128)
 
 # scalar registers owned by the body (all callee state lives in these)
 S_KDMA = 60      # s[60:61] K DMA base (bytes) of tile min(kt+2, nkt-1)
@@ -71,10 +94,6 @@ S_EXEC = 72      # s[72:73] saved exec
 S_VALID = 74     # s74 valid keys of the last tile
 S_THR = 75       # s75 the lazy-rescale threshold 256.0
 SGPRS = list(range(60, 76))
-
-BN, HD = 64, 128
-KSTAGE_BYTES = BN * HD * 2     # 16 KiB
-VSTAGE_BYTES = HD * BN * 2     # 16 KiB
 
 
 def s_(n):
@@ -103,11 +122,11 @@ def p_reg(setv, qb, g, e=0):
 
 
 def o_reg(qb, d):
-    return O_A + (qb * 4 + d) * 16
+    return O_A + (qb * DT + d) * 16
 
 
 def q_reg(qb, c):
-    return Q_A + (qb * 8 + c) * 4
+    return Q_A + (qb * NC + c) * 4
 
 
 def kf_reg(r, kk):
@@ -223,14 +242,14 @@ def vdma_go(g, i):
 
 
 def kdma_block(g, stage):
-    for i in range(4):
+    for i in range(ND):
         kdma_m0(g, i, stage)
         g("s_nop 0")
         kdma_go(g, i)
 
 
 def vdma_block(g, stage):
-    for i in range(4):
+    for i in range(ND):
         vdma_m0(g, i, stage)
         g("s_nop 0")
         vdma_go(g, i)
@@ -242,7 +261,7 @@ def clamp_koff(g, cmp):
     skip = g.new_label("noclamp")
     g(cmp)
     g(f"s_cbranch_scc0 {skip}")
-    for i in range(4):
+    for i in range(ND):
         g(f"v_mov_b32 {vr(KOFF + i)}, %[koffl{i}]")
     g.label(skip)
 
@@ -255,7 +274,7 @@ def k_read(g, chunk, kk, stage):
 
 
 def v_read(g, f, stage):
-    grp, d = f // 4, f % 4
+    grp, d = f // DT, f % DT
     g(f"ds_read_b128 {ar(vf_reg(f % VRING), 4)}, %[vaddr{grp}] offset:{stage * VSTAGE_BYTES + d * 4096}")
     g.lds_issue(("v", f))
 
@@ -278,7 +297,7 @@ def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None):
     one callable per slot; dma: (before, after) callables around the MFMA of the
     first slots."""
     slot = 0
-    for c in range(8):
+    for c in range(NC):
         g.lds_wait(("k", c, 1))
         for kk in range(2):
             for qb in range(2):
@@ -286,10 +305,10 @@ def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None):
                 if d:
                     d[0]()
                 mfma_s(g, s_set, qb, kk, c)
-                if kk == 0 and qb == 0 and c + 2 < 8:
+                if kk == 0 and qb == 0 and c + 2 < NC:
                     k_read(g, c + 2, 0, kstage)
                     k_read(g, c + 2, 1, kstage)
-                if kk == 0 and qb == 0 and c == 7 and vstage is not None:
+                if kk == 0 and qb == 0 and c == NC - 1 and vstage is not None:
                     for f in range(4):
                         v_read(g, f, vstage)
                 if d:
@@ -303,13 +322,13 @@ def o_phase(g, p_set, vstage, items=None):
     """32 PV MFMAs with Vt fragments of stage vstage four ahead (the first four
     already issued), waited for in pairs."""
     slot = 0
-    for f in range(16):
-        grp, d = f // 4, f % 4
+    for f in range(NF):
+        grp, d = f // DT, f % DT
         for qb in range(2):
             if qb == 0 and f % 2 == 0:
                 g.lds_wait(("v", f + 1))
             mfma_o(g, p_set, qb, d, grp, f % VRING)
-            if qb == 0 and f + 4 < 16:
+            if qb == 0 and f + 4 < NF:
                 v_read(g, f + 4, vstage)
             if items is not None:
                 items[slot]()
@@ -345,7 +364,7 @@ def row_max_to(g, s_set, qb, dst, tmp):
 
 
 def scale_o(g, qb, alpha):
-    for d in range(4):
+    for d in range(DT):
         for v in range(16):
             a = o_reg(qb, d) + v
             g(f"v_accvgpr_read_b32 {vr(DTMP)}, {ar(a)}")
@@ -414,7 +433,7 @@ def tile(g, a):
     after_check = g.new_label("checked")
     resc = g.new_label("rescale")
     g.lds = [("k", 0, 0), ("k", 0, 1), ("k", 1, 0), ("k", 1, 1)]
-    # K DMA base of tile min(kt+2, nkt-1); the last tile's rows past the end clamp
+    # K DMA source of tile min(kt+2, nkt-1); the last tile's rows past the end clamp
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 2")
     g(f"s_min_u32 {s_(S_T0)}, {s_(S_T0)}, {s_(S_NKT1)}")
     g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
@@ -422,10 +441,10 @@ def tile(g, a):
     g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
     g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
     clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
-    dmas = ([(lambda i=i: kdma_m0(g, i, a), lambda i=i: kdma_go(g, i)) for i in range(4)] +
-            [(lambda i=i: vdma_m0(g, i, b), lambda i=i: vdma_go(g, i)) for i in range(4)])
+    dmas = ([(lambda i=i: kdma_m0(g, i, a), lambda i=i: kdma_go(g, i)) for i in range(ND)] +
+            [(lambda i=i: vdma_m0(g, i, b), lambda i=i: vdma_go(g, i)) for i in range(ND)])
     # phase 1: S(kt+1) into set b || P(kt) keys 32..63 from set a
-    items = make_items(g, pair_list(1), a, a, RS1)
+    items = make_items(g, pair_list(1), a, a, RS1, slots=4 * NC)
     s_phase(g, b, kstage=b, vstage=a, items=items, dma=dmas)
     # lazy-rescale check on tile kt: rsum = rs0 + rs1 (per lane), flag !(rsum <= 256)
     for qb in range(2):
@@ -441,7 +460,7 @@ def tile(g, a):
     # covers the VALU reads of the S(kt+1) results of the last MFMAs (already
     # three MFMAs old) and the MFMA reads of the P(kt) just packed.
     g.nops(2)
-    items = make_items(g, pair_list(0), b, b, RS0)
+    items = make_items(g, pair_list(0), b, b, RS0, slots=2 * NF)
     o_phase(g, a, vstage=a, items=items)
     # publish this tile's DMA: own loads landed, then the workgroup barrier
     g("s_waitcnt vmcnt(0)")
@@ -521,9 +540,9 @@ def prologue(g):
     # (K stage 1; K(0) again when there is one tile) and Vt(0) (Vt stage 0), all
     # before the first wait so that their latencies overlap
     for qb in range(2):
-        for c in range(8):
+        for c in range(NC):
             g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, %[qoff{qb}], %[qbase] offset:{c * 32}")
-    for i in range(4):
+    for i in range(ND):
         g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
     g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
     g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
@@ -539,14 +558,14 @@ def prologue(g):
     g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
     g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
     # O = 0, l = 0 while the loads fly
-    for i in range(128):
+    for i in range(2 * DT * 16):
         g(f"v_accvgpr_write_b32 {ar(O_A + i)}, 0")
     for qb in range(2):
         g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
         g(f"v_mov_b32 {vr(RS1 + qb)}, 0")
-    # Q and K(0) landed (the 8 DMAs of K(1) and Vt(0) may still fly), K(0) published
-    g("s_waitcnt vmcnt(8)")
+    # Q and K(0) landed (the DMAs of K(1) and Vt(0) may still fly), K(0) published
+    g(f"s_waitcnt vmcnt({2 * ND})")
     g("s_barrier")
     # S(0) = K(0) Q^T into set A
     g.lds = []
@@ -605,7 +624,7 @@ def epilogue(g):
         g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(addr + 2)}, {vr(addr + 1)}, vcc")
         g(f"v_add_co_u32 {vr(addr)}, vcc, %[hh8], {vr(addr)}")
         g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
-        for d in range(4):
+        for d in range(DT):
             for gg in range(4):
                 w0, w1 = 4, 5
                 base = o_reg(qb, d) + gg * 4
@@ -670,25 +689,32 @@ def generate():
     return g.lines
 
 
-def clobbers():
+def clobbers(hd):
+    configure(hd)
     regs = ([f"v{i}" for i in range(LAST_VGPR + 1)] + [f"a{i}" for i in range(LAST_AGPR + 1)] +
             [f"s{i}" for i in SGPRS])
     rows = [", ".join(f'"{r}"' for r in regs[i:i + 16]) for i in range(0, len(regs), 16)]
-    return ("// Registers the generated flash_fwd_d128 body owns (gen_attn_d128.py register map).\n"
-            "#define DITK_D128_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
+    return (f"// Registers the generated flash_fwd_asm<{hd}> body owns (gen_attn.py register map).\n"
+            f"#define DITK_D{hd}_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
+
+
+def write_body(path, hd):
+    configure(hd)
+    lines = generate()
+    with open(path, "w") as f:
+        f.write(f"// Generated by gen_attn.py -- the instruction body of flash_fwd_asm<{hd}>.\n")
+        for line in lines:
+            esc = line.replace("\\", "\\\\").replace('"', '\\"')
+            f.write(f'"{esc}\\n"\n')
 
 
 def main(argv):
     here = os.path.dirname(os.path.abspath(__file__))
-    out = argv[1] if len(argv) > 1 else os.path.join(here, "attn_d128_body.inc")
-    lines = generate()
-    with open(out, "w") as f:
-        f.write("// Generated by gen_attn_d128.py -- the instruction body of flash_fwd_d128.\n")
-        for line in lines:
-            esc = line.replace("\\", "\\\\").replace('"', '\\"')
-            f.write(f'"{esc}\\n"\n')
-    with open(os.path.join(os.path.dirname(os.path.abspath(out)), "attn_d128_clobbers.h"), "w") as f:
-        f.write(clobbers())
+    out = os.path.dirname(os.path.abspath(argv[1])) if len(argv) > 1 else here
+    for hd in (128, 64):
+        write_body(os.path.join(out, f"attn_d{hd}_body.inc"), hd)
+        with open(os.path.join(out, f"attn_d{hd}_clobbers.h"), "w") as f:
+            f.write(clobbers(hd))
     return 0
 
 

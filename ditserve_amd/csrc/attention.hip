@@ -46,7 +46,9 @@
 
 #include "ditk_common.h"
 #include "attn_d128_clobbers.h"
+#include "attn_d128p_clobbers.h"
 #include "attn_d64_clobbers.h"
+#include "attn_d64p_clobbers.h"
 
 namespace {
 
@@ -696,7 +698,22 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [koffl0] "v"(koffl[0]), [koffl1] "v"(koffl[1]), [koffl2] "v"(koffl[2]), [koffl3] "v"(koffl[3]),             \
       [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
       [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0), [qrow1] "v"(qrow1)
-template <int HD>
+// Pre-scaled q: the body's -m blocks take 32 more VGPRs, so the per-lane values
+// it reads only outside the key loop arrive in AGPRs
+#define DITK_ATTN_ASM_OPERANDS_PRE                                                                                  \
+  [qbase] "s"(su64(qbase)), [qoff0] "a"(qoff0), [qoff1] "a"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),            \
+      [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
+      [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
+      [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
+      [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),                           \
+      [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
+      [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
+      [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
+      [koff0] "a"(koff[0]), [koff1] "a"(koff[1]), [koff2] "a"(koff[2]), [koff3] "a"(koff[3]),                     \
+      [koffl0] "a"(koffl[0]), [koffl1] "a"(koffl[1]), [koffl2] "a"(koffl[2]), [koffl3] "a"(koffl[3]),             \
+      [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
+      [xaddr] "a"(xaddr), [hh8] "a"(hh8), [lane] "a"(lanev), [qrow0] "a"(qrow0), [qrow1] "a"(qrow1)
+template <int HD, bool PRE>
 __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
@@ -720,17 +737,8 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   const int q_end = cu_q[seg + 1];
   const int qrow0 = cu_q[seg] + t * BM + wave * 64 + l32;
   const int qrow1 = qrow0 + 32;
-  const int k_beg = cu_k[seg], k_len = cu_k[seg + 1] - k_beg;
-  if (k_len <= 0) {  // no keys: zero output rows, lse -inf (nothing to attend)
-    for (int qb = 0; qb < 2; ++qb) {
-      const int qrow = qb ? qrow1 : qrow0;
-      if (qrow < q_end) {
-        for (int d = hh * (HD / 2); d < (hh + 1) * (HD / 2); ++d) O[(int64_t)qrow * ldo + (int64_t)head * HD + d] = 0;
-        if (lse != nullptr && hh == 0) lse[(int64_t)head * lse_ld + qrow] = -INFINITY;
-      }
-    }
-    return;
-  }
+  const int k_beg = cu_k[seg], k_len = max(cu_k[seg + 1] - k_beg, 0);
+  // nkt == 0 (no keys): the body stores zero rows and lse = -inf, issuing no DMA
   const int nkt = (k_len + BN - 1) / BN;
   const int valid_last = k_len - (nkt - 1) * BN;
   const int pk = padded_key_start(cu_k, seg);
@@ -780,14 +788,24 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   auto su = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
   auto su64 = [&](uint64_t x) { return ((uint64_t)su((uint32_t)(x >> 32)) << 32) | su((uint32_t)x); };
   const float sc = __builtin_bit_cast(float, su(__builtin_bit_cast(uint32_t, scale_log2)));
-  if constexpr (HD == 128) {
+  if constexpr (HD == 128 && !PRE) {
     asm volatile(
 #include "attn_d128_body.inc"
         : : DITK_ATTN_ASM_OPERANDS : DITK_D128_CLOBBERS "vcc", "scc", "memory");
-  } else {
+  } else if constexpr (HD == 64 && !PRE) {
     asm volatile(
 #include "attn_d64_body.inc"
         : : DITK_ATTN_ASM_OPERANDS : DITK_D64_CLOBBERS "vcc", "scc", "memory");
+  } else if constexpr (HD == 128) {
+    (void)sc;
+    asm volatile(
+#include "attn_d128p_body.inc"
+        : : DITK_ATTN_ASM_OPERANDS_PRE : DITK_D128P_CLOBBERS "vcc", "scc", "memory");
+  } else {
+    (void)sc;
+    asm volatile(
+#include "attn_d64p_body.inc"
+        : : DITK_ATTN_ASM_OPERANDS_PRE : DITK_D64P_CLOBBERS "vcc", "scc", "memory");
   }
 }
 
@@ -926,8 +944,6 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
   int rc;
   if (joint)
     rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, true>, kWaves * kQBlocks * 32, kWaves * 64);
-  else if (pre)
-    rc = run(flash_fwd_kernel<64, kWaves, kQBlocks, true, false>, kWaves * kQBlocks * 32, kWaves * 64);
   else {
     // one wave per SIMD, 64 queries per wave: generated-assembly body
     DITK_REQUIRE((int64_t)Tq * ldq * 2 < (1ll << 32) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
@@ -936,7 +952,8 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     int64_t nblocks = (int64_t)tiles_bound * heads;
     nblocks = (nblocks + 7) / 8 * 8;
     DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
-    auto kern = head_dim == 128 ? flash_fwd_asm<128> : flash_fwd_asm<64>;
+    auto kern = head_dim == 128 ? (pre ? flash_fwd_asm<128, true> : flash_fwd_asm<128, false>)
+                                : (pre ? flash_fwd_asm<64, true> : flash_fwd_asm<64, false>);
     kern<<<(unsigned)nblocks, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk, (const bf16_t*)vt,
                                                 vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld, cu_q, cu_k, nseg, heads,
                                                 tiles_bound, sl2);
@@ -962,7 +979,6 @@ DITK_EXPORT int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, c
                                                    float* lse, int64_t lse_ld, const int32_t* cu_q,
                                                    const int32_t* cu_k, int nseg, int Tq, int heads,
                                                    int head_dim, hipStream_t stream) {
-  DITK_REQUIRE(head_dim == 64, "ditk_flash_attn_varlen_q_prescaled: head_dim must be 64, got %d", head_dim);
   return flash_launch(q, ldq, k, ldk, vt, vt_ld, o, ldo, lse, lse_ld, cu_q, cu_k, nseg, Tq, heads, head_dim,
                       1.0f, true, stream);
 }

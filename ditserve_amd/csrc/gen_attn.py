@@ -53,21 +53,37 @@ import sys
 # register map (VGPRs: the same for both head dims)
 S_SET = (0, 64)
 P_SET = (128, 160)
-TMP = 192
-RS0, RS1, NEGM, LRUN = 200, 202, 204, 206
-KOFF, DTMP = 208, 212
 VRING = 6        # Vt fragment ring (read four fragments ahead)
-LAST_VGPR = 215
 BN = 64
 
 
-def configure(hd):
+def configure(hd, pre=False):
     """Head dim 128 or 64: NC 16-wide chunks of the head dim (K fragments per key
     half), DT 32-row d tiles of O^T, NF Vt fragments per tile (4 key groups x DT),
     ND DMA instructions per wave and operand per tile; AGPRs: O^T, then Q, the K
-    ring (3 chunks x 2 key halves) and the Vt ring."""
+    ring (3 chunks x 2 key halves) and the Vt ring.
+
+    pre: q arrives multiplied by softmax_scale * log2(e), and the first MFMA of
+    every S accumulator starts from a block of 16 registers holding -m (one block
+    per query block, v210..v241), so S is already q.k - m in log2 units and
+    P = exp2(S) needs no per-score fma.  The VGPRs for the blocks come from a
+    two-pair exp ring with the tile temporaries above it, no separate -m
+    registers, and the per-lane operands used only outside the loop (Q and K DMA
+    offsets, output rows, lane constants) passed in AGPRs."""
     global HD, NC, DT, NF, ND, KSTAGE_BYTES, VSTAGE_BYTES, O_A, Q_A, KF_A, VF_A, LAST_AGPR
-    HD = hd
+    global PRE, TMP, RING, DTMP, RS0, RS1, NEGM, NEGB, LRUN, KOFF, LAST_VGPR, EPI_T, EPI_L
+    HD, PRE = hd, pre
+    TMP = 192
+    if pre:
+        RING, DTMP = 2, 196
+        RS0, RS1, LRUN, KOFF, NEGB, NEGM = 200, 202, 204, 206, 210, None
+        LAST_VGPR = 241
+        EPI_T, EPI_L = 64, 70          # epilogue temporaries in S set B (dead there)
+    else:
+        RING = 4                       # exp temporaries: a ring of four score pairs
+        RS0, RS1, NEGM, LRUN, KOFF, DTMP, NEGB = 200, 202, 204, 206, 208, 212, None
+        LAST_VGPR = 215
+        EPI_T, EPI_L = TMP, DTMP
     NC, DT = hd // 16, hd // 32
     NF = 4 * DT
     ND = hd // 32
@@ -98,6 +114,20 @@ SGPRS = list(range(60, 76))
 
 def s_(n):
     return f"s{n}"
+
+
+def negm(qb):
+    """The register holding -m of query block qb (the first of its block when pre)."""
+    return NEGB + 16 * qb if PRE else NEGM + qb
+
+
+def opnd(g, name, tmp):
+    """A per-lane operand as a VGPR operand string: when pre it arrives in an AGPR
+    and is copied to VGPR tmp first."""
+    if PRE:
+        g(f"v_accvgpr_read_b32 {vr(tmp)}, %[{name}]")
+        return vr(tmp)
+    return f"%[{name}]"
 
 
 def sp(n):
@@ -205,14 +235,18 @@ def emit_half(g, half, pi, pair, s_set, p_set, rs_base):
     P, and the row sum rs += (p0 + p1).  The first pair of a query block starts
     the sum (rs = p0 + p1, the same value as 0 + (p0 + p1))."""
     qb, kk, j, e = pair
-    t0 = TMP + 2 * (pi % 4)
+    t0 = TMP + 2 * (pi % RING)
     t1 = t0 + 1
     if half == 0:
         s0 = s_reg(s_set, qb, kk, j * 8 + 2 * e)
-        g(f"v_fma_f32 {vr(t0)}, {vr(s0)}, %[sc], {vr(NEGM + qb)}")
-        g(f"v_fma_f32 {vr(t1)}, {vr(s0 + 1)}, %[sc], {vr(NEGM + qb)}")
-        g(f"v_exp_f32 {vr(t0)}, {vr(t0)}")
-        g(f"v_exp_f32 {vr(t1)}, {vr(t1)}")
+        if PRE:
+            g(f"v_exp_f32 {vr(t0)}, {vr(s0)}")
+            g(f"v_exp_f32 {vr(t1)}, {vr(s0 + 1)}")
+        else:
+            g(f"v_fma_f32 {vr(t0)}, {vr(s0)}, %[sc], {vr(NEGM + qb)}")
+            g(f"v_fma_f32 {vr(t1)}, {vr(s0 + 1)}, %[sc], {vr(NEGM + qb)}")
+            g(f"v_exp_f32 {vr(t0)}, {vr(t0)}")
+            g(f"v_exp_f32 {vr(t1)}, {vr(t1)}")
     else:
         g(f"v_cvt_pk_bf16_f32 {vr(p_reg(p_set, qb, kk * 2 + j, e))}, {vr(t0)}, {vr(t1)}")
         if j == 0 and e == 0:
@@ -262,7 +296,10 @@ def clamp_koff(g, cmp):
     g(cmp)
     g(f"s_cbranch_scc0 {skip}")
     for i in range(ND):
-        g(f"v_mov_b32 {vr(KOFF + i)}, %[koffl{i}]")
+        if PRE:
+            g(f"v_accvgpr_read_b32 {vr(KOFF + i)}, %[koffl{i}]")
+        else:
+            g(f"v_mov_b32 {vr(KOFF + i)}, %[koffl{i}]")
     g.label(skip)
 
 
@@ -279,9 +316,13 @@ def v_read(g, f, stage):
     g.lds_issue(("v", f))
 
 
-def mfma_s(g, s_set, qb, kk, chunk):
+def mfma_s(g, s_set, qb, kk, chunk, first=False):
+    """first: the prologue's S(0), started from 0 also when pre (m not known yet)."""
     dst = s_reg(s_set, qb, kk)
-    src_c = "0" if chunk == 0 else vr(dst, 16)
+    if chunk > 0:
+        src_c = vr(dst, 16)
+    else:
+        src_c = vr(negm(qb), 16) if PRE and not first else "0"
     g(f"v_mfma_f32_32x32x16_bf16 {vr(dst, 16)}, {ar(kf_reg(chunk % 3, kk), 4)}, {ar(q_reg(qb, chunk), 4)}, {src_c}")
 
 
@@ -290,7 +331,7 @@ def mfma_o(g, p_set, qb, d, grp, ring):
     g(f"v_mfma_f32_32x32x16_bf16 {ar(o, 16)}, {ar(vf_reg(ring), 4)}, {vr(p_reg(p_set, qb, grp), 4)}, {ar(o, 16)}")
 
 
-def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None):
+def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None, first=False):
     """32 S MFMAs (into s_set) with K fragments of K stage kstage read two chunks
     ahead; the first two chunks' reads must already be issued.  vstage: issue the
     first four Vt reads of that stage after the last chunk's first MFMA.  items:
@@ -304,7 +345,7 @@ def s_phase(g, s_set, kstage, vstage=None, items=None, dma=None):
                 d = dma[slot] if dma is not None and slot < len(dma) else None
                 if d:
                     d[0]()
-                mfma_s(g, s_set, qb, kk, c)
+                mfma_s(g, s_set, qb, kk, c, first)
                 if kk == 0 and qb == 0 and c + 2 < NC:
                     k_read(g, c + 2, 0, kstage)
                     k_read(g, c + 2, 1, kstage)
@@ -346,9 +387,10 @@ def make_items(g, pairs, s_set, p_set, rs_base, slots=32):
     return [fn(x) for x in per]
 
 
-def row_max_to(g, s_set, qb, dst, tmp):
+def row_max_to(g, s_set, qb, dst, tmp, atmp):
     """dst = max over this lane's 32 scores of query block qb (both half-waves
-    combined), times the softmax scale (log2 units)."""
+    combined), times the softmax scale (log2 units; pre: the scores already are).
+    atmp: a VGPR for the exchange address when it arrives in an AGPR."""
     base = s_reg(s_set, qb, 0)
     g(f"v_max3_f32 {vr(dst)}, {vr(base)}, {vr(base + 16)}, {vr(base + 1)}")
     for v in range(1, 16):
@@ -357,10 +399,12 @@ def row_max_to(g, s_set, qb, dst, tmp):
             g(f"v_max_f32 {vr(dst)}, {vr(dst)}, {vr(b)}")
         else:
             g(f"v_max3_f32 {vr(dst)}, {vr(dst)}, {vr(a)}, {vr(b)}")
-    g(f"ds_bpermute_b32 {vr(tmp)}, %[xaddr], {vr(dst)}")
+    xa = opnd(g, "xaddr", atmp)
+    g(f"ds_bpermute_b32 {vr(tmp)}, {xa}, {vr(dst)}")
     g("s_waitcnt lgkmcnt(0)")
     g(f"v_max_f32 {vr(dst)}, {vr(dst)}, {vr(tmp)}")
-    g(f"v_mul_f32 {vr(dst)}, %[sc], {vr(dst)}")
+    if not PRE:
+        g(f"v_mul_f32 {vr(dst)}, %[sc], {vr(dst)}")
 
 
 def scale_o(g, qb, alpha):
@@ -374,16 +418,22 @@ def scale_o(g, qb, alpha):
 
 def softmax_tile(g, s_set, p_set, qb, kks, rs_dst, masked=False):
     """Recompute P for the given key halves of query block qb from the raw scores
-    and the running m; rs_dst += sum (masked: keys >= valid excluded)."""
+    and the running m (pre: from S = q.k - m); rs_dst += sum (masked: keys >=
+    valid excluded)."""
+    hh8 = opnd(g, "hh8", TMP + 3) if masked else None
     for kk in kks:
         for j in range(2):
             for e in range(4):
                 s0 = s_reg(s_set, qb, kk, j * 8 + 2 * e)
                 t0, t1 = TMP, TMP + 1
-                g(f"v_fma_f32 {vr(t0)}, {vr(s0)}, %[sc], {vr(NEGM + qb)}")
-                g(f"v_fma_f32 {vr(t1)}, {vr(s0 + 1)}, %[sc], {vr(NEGM + qb)}")
-                g(f"v_exp_f32 {vr(t0)}, {vr(t0)}")
-                g(f"v_exp_f32 {vr(t1)}, {vr(t1)}")
+                if PRE:
+                    g(f"v_exp_f32 {vr(t0)}, {vr(s0)}")
+                    g(f"v_exp_f32 {vr(t1)}, {vr(s0 + 1)}")
+                else:
+                    g(f"v_fma_f32 {vr(t0)}, {vr(s0)}, %[sc], {vr(NEGM + qb)}")
+                    g(f"v_fma_f32 {vr(t1)}, {vr(s0 + 1)}, %[sc], {vr(NEGM + qb)}")
+                    g(f"v_exp_f32 {vr(t0)}, {vr(t0)}")
+                    g(f"v_exp_f32 {vr(t1)}, {vr(t1)}")
                 g("s_nop 0")
                 g(f"v_cvt_pk_bf16_f32 {vr(p_reg(p_set, qb, kk * 2 + j, e))}, {vr(t0)}, {vr(t1)}")
                 if masked:
@@ -391,33 +441,52 @@ def softmax_tile(g, s_set, p_set, qb, kks, rs_dst, masked=False):
                     # keep p where key (+1) < valid, i.e. hh8 < valid - key (- 1)
                     for t, kk_off in ((t0, 0), (t1, 1)):
                         g(f"s_sub_i32 {s_(S_T0)}, {s_(S_VALID)}, {key + kk_off}")
-                        g(f"v_cmp_gt_i32 vcc, {s_(S_T0)}, %[hh8]")
+                        g(f"v_cmp_gt_i32 vcc, {s_(S_T0)}, {hh8}")
                         g(f"v_cndmask_b32 {vr(t)}, 0, {vr(t)}, vcc")
                 g(f"v_add_f32 {vr(t0)}, {vr(t0)}, {vr(t1)}")
                 g(f"v_add_f32 {vr(rs_dst + qb)}, {vr(rs_dst + qb)}, {vr(t0)}")
 
 
-def exact_rescale(g, s_set, p_set, kks, masked=False):
+def exact_rescale(g, s_set, p_set, kks, masked=False, live_next=None):
     """The C++ rescale: m_new = max(m, row max of the tile's scores), O and l
     scaled by exp2(m - m_new), P of the tile recomputed against m_new into rs0.
-    (rs1 is cleared.)"""
+    (rs1 is cleared.)  Pre: the scores are relative to m_old, so m_new = max(m_old,
+    row max + m_old); the tile's S and the next tile's (S set live_next, started
+    from the old -m block) move by -(m_new - m_old) and the block becomes -m_new."""
     g.nops(20)  # O accumulators read below: MFMA results must have landed
     for qb in range(2):
         mx, tmp, alpha = DTMP + 1, DTMP + 2, DTMP + 3
-        row_max_to(g, s_set, qb, mx, tmp)
-        # m_old = -negm ; m_new = max(m_old, mx) ; alpha = exp2(m_old - m_new)
-        g(f"v_sub_f32 {vr(tmp)}, 0, {vr(NEGM + qb)}")        # m_old
-        g(f"v_max_f32 {vr(mx)}, {vr(tmp)}, {vr(mx)}")         # m_new
-        g(f"v_sub_f32 {vr(alpha)}, {vr(tmp)}, {vr(mx)}")
-        g(f"v_exp_f32 {vr(alpha)}, {vr(alpha)}")
-        g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(mx)}")
+        row_max_to(g, s_set, qb, mx, tmp, alpha)
+        if PRE:
+            nb = negm(qb)
+            g(f"v_sub_f32 {vr(tmp)}, 0, {vr(nb)}")            # m_old
+            g(f"v_add_f32 {vr(mx)}, {vr(mx)}, {vr(tmp)}")     # row max + m_old
+            g(f"v_max_f32 {vr(mx)}, {vr(tmp)}, {vr(mx)}")     # m_new
+            g(f"v_sub_f32 {vr(alpha)}, {vr(tmp)}, {vr(mx)}")
+            g(f"v_exp_f32 {vr(alpha)}, {vr(alpha)}")
+            g(f"v_sub_f32 {vr(tmp)}, {vr(mx)}, {vr(tmp)}")    # m_new - m_old
+            g(f"v_sub_f32 {vr(mx)}, 0, {vr(mx)}")
+            for v in range(16):
+                g(f"v_mov_b32 {vr(nb + v)}, {vr(mx)}")
+            for st in (s_set,) if live_next is None else (s_set, live_next):
+                for kk in (kks if st == s_set else (0, 1)):
+                    for v in range(16):
+                        r = s_reg(st, qb, kk, v)
+                        g(f"v_sub_f32 {vr(r)}, {vr(r)}, {vr(tmp)}")
+        else:
+            # m_old = -negm ; m_new = max(m_old, mx) ; alpha = exp2(m_old - m_new)
+            g(f"v_sub_f32 {vr(tmp)}, 0, {vr(NEGM + qb)}")        # m_old
+            g(f"v_max_f32 {vr(mx)}, {vr(tmp)}, {vr(mx)}")         # m_new
+            g(f"v_sub_f32 {vr(alpha)}, {vr(tmp)}, {vr(mx)}")
+            g(f"v_exp_f32 {vr(alpha)}, {vr(alpha)}")
+            g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(mx)}")
         g("s_nop 0")
         g(f"v_mul_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(alpha)}")
         scale_o(g, qb, alpha)
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
         g(f"v_mov_b32 {vr(RS1 + qb)}, 0")
         softmax_tile(g, s_set, p_set, qb, kks, RS0, masked)
-    g.nops(3)  # v_accvgpr_write -> MFMA srcC
+    g.nops(5 if PRE else 3)  # v_accvgpr_write (and the -m block writes) -> MFMA srcC
 
 
 def tile(g, a):
@@ -479,7 +548,7 @@ def rescale_block(g, a, resc, back):
     """Out-of-line rescale of tile kt (scores still in set a, P(kt) in P set a);
     returns with the tile's row sums in DTMP like the common path."""
     g.label(resc)
-    exact_rescale(g, a, a, (0, 1))
+    exact_rescale(g, a, a, (0, 1), live_next=1 - a)
     for qb in range(2):
         g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
     g(f"s_branch {back}")
@@ -526,7 +595,9 @@ def last_tile(g, a):
     o_phase(g, a, vstage=a, items=None)
 
 
-def prologue(g):
+def prologue(g, empty):
+    """empty: the label of the no-keys exit (O = 0, l = 0: the epilogue then
+    stores zero rows and lse = -inf)."""
     # scalar state
     g(f"s_mov_b32 {s_(S_VDMA)}, %[vdma_lo]")
     g(f"s_mov_b32 {s_(S_VDMA + 1)}, %[vdma_hi]")
@@ -536,14 +607,22 @@ def prologue(g):
     g(f"s_sub_u32 {s_(S_NKT1)}, %[nkt], 1")
     g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
     g(f"s_mov_b32 {s_(S_THR)}, 0x43800000")
+    g("s_cmp_eq_u32 %[nkt], 0")
+    g(f"s_cbranch_scc1 {empty}")
     # Q fragments straight into AGPRs, then the DMAs of K(0) (K stage 0), K(1)
     # (K stage 1; K(0) again when there is one tile) and Vt(0) (Vt stage 0), all
     # before the first wait so that their latencies overlap
+    if PRE:
+        g("s_nop 4")  # the AGPR operands were written just before the body
     for qb in range(2):
+        qo = opnd(g, f"qoff{qb}", S_SET[0] + qb)
         for c in range(NC):
-            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, %[qoff{qb}], %[qbase] offset:{c * 32}")
+            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {qo}, %[qbase] offset:{c * 32}")
     for i in range(ND):
-        g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
+        if PRE:
+            g(f"v_accvgpr_read_b32 {vr(KOFF + i)}, %[koff{i}]")
+        else:
+            g(f"v_mov_b32 {vr(KOFF + i)}, %[koff{i}]")
     g(f"s_mov_b32 {s_(S_KDMA)}, %[kdma_lo]")
     g(f"s_mov_b32 {s_(S_KDMA + 1)}, %[kdma_hi]")
     clamp_koff(g, f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
@@ -572,12 +651,21 @@ def prologue(g):
     for c in range(2):
         k_read(g, c, 0, 0)
         k_read(g, c, 1, 0)
-    s_phase(g, 0, kstage=0)
+    s_phase(g, 0, kstage=0, first=True)
     g.nops(20)
-    # m = exact max of tile 0
+    # m = exact max of tile 0 (pre: S(0) -= m, and the -m blocks)
     for qb in range(2):
-        row_max_to(g, 0, qb, DTMP + 1, DTMP + 2)
-        g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(DTMP + 1)}")
+        row_max_to(g, 0, qb, DTMP + 1, DTMP + 2, DTMP + 3)
+        if PRE:
+            for kk in range(2):
+                for v in range(16):
+                    r = s_reg(0, qb, kk, v)
+                    g(f"v_sub_f32 {vr(r)}, {vr(r)}, {vr(DTMP + 1)}")
+            g(f"v_sub_f32 {vr(DTMP + 1)}, 0, {vr(DTMP + 1)}")
+            for v in range(16):
+                g(f"v_mov_b32 {vr(negm(qb) + v)}, {vr(DTMP + 1)}")
+        else:
+            g(f"v_sub_f32 {vr(NEGM + qb)}, 0, {vr(DTMP + 1)}")
     g("s_waitcnt vmcnt(0)")
     g("s_barrier")
     # tile 0 reads K(1) from K stage 1; its first reads are issued here
@@ -590,39 +678,43 @@ def prologue(g):
 def epilogue(g):
     """l total over both half-waves, O / l to bf16, stores; lse when asked."""
     g.nops(20)
+    T = EPI_T
     for qb in range(2):
-        lt, inv, t = DTMP + 0, DTMP + 1, DTMP + 2
-        g(f"ds_bpermute_b32 {vr(t)}, %[xaddr], {vr(LRUN + qb)}")
+        lt, inv, t = EPI_L + 0, EPI_L + 1, EPI_L + 2
+        xa = opnd(g, "xaddr", EPI_L + 3)
+        qrow = opnd(g, f"qrow{qb}", EPI_L + 4)
+        g(f"ds_bpermute_b32 {vr(t)}, {xa}, {vr(LRUN + qb)}")
         g("s_waitcnt lgkmcnt(0)")
         g(f"v_add_f32 {vr(lt)}, {vr(LRUN + qb)}, {vr(t)}")
         # inv = l > 0 ? 1 / l : 0  (IEEE division sequence)
-        g(f"v_div_scale_f32 {vr(TMP)}, {sp(S_CMP)}, {vr(lt)}, {vr(lt)}, 1.0")
-        g(f"v_rcp_f32 {vr(TMP + 1)}, {vr(TMP)}")
+        g(f"v_div_scale_f32 {vr(T)}, {sp(S_CMP)}, {vr(lt)}, {vr(lt)}, 1.0")
+        g(f"v_rcp_f32 {vr(T + 1)}, {vr(T)}")
         g("s_nop 0")
-        g(f"v_fma_f32 {vr(TMP + 2)}, -{vr(TMP)}, {vr(TMP + 1)}, 1.0")
-        g(f"v_fmac_f32 {vr(TMP + 1)}, {vr(TMP + 2)}, {vr(TMP + 1)}")
-        g(f"v_div_scale_f32 {vr(TMP + 3)}, vcc, 1.0, {vr(lt)}, 1.0")
-        g(f"v_mul_f32 {vr(TMP + 4)}, {vr(TMP + 3)}, {vr(TMP + 1)}")
-        g(f"v_fma_f32 {vr(TMP + 5)}, -{vr(TMP)}, {vr(TMP + 4)}, {vr(TMP + 3)}")
-        g(f"v_fmac_f32 {vr(TMP + 4)}, {vr(TMP + 5)}, {vr(TMP + 1)}")
-        g(f"v_fma_f32 {vr(TMP + 3)}, -{vr(TMP)}, {vr(TMP + 4)}, {vr(TMP + 3)}")
-        g(f"v_div_fmas_f32 {vr(TMP + 3)}, {vr(TMP + 3)}, {vr(TMP + 1)}, {vr(TMP + 4)}")
-        g(f"v_div_fixup_f32 {vr(inv)}, {vr(TMP + 3)}, {vr(lt)}, 1.0")
+        g(f"v_fma_f32 {vr(T + 2)}, -{vr(T)}, {vr(T + 1)}, 1.0")
+        g(f"v_fmac_f32 {vr(T + 1)}, {vr(T + 2)}, {vr(T + 1)}")
+        g(f"v_div_scale_f32 {vr(T + 3)}, vcc, 1.0, {vr(lt)}, 1.0")
+        g(f"v_mul_f32 {vr(T + 4)}, {vr(T + 3)}, {vr(T + 1)}")
+        g(f"v_fma_f32 {vr(T + 5)}, -{vr(T)}, {vr(T + 4)}, {vr(T + 3)}")
+        g(f"v_fmac_f32 {vr(T + 4)}, {vr(T + 5)}, {vr(T + 1)}")
+        g(f"v_fma_f32 {vr(T + 3)}, -{vr(T)}, {vr(T + 4)}, {vr(T + 3)}")
+        g(f"v_div_fmas_f32 {vr(T + 3)}, {vr(T + 3)}, {vr(T + 1)}, {vr(T + 4)}")
+        g(f"v_div_fixup_f32 {vr(inv)}, {vr(T + 3)}, {vr(lt)}, 1.0")
         g(f"v_cmp_lt_f32 vcc, 0, {vr(lt)}")
         g(f"v_cndmask_b32 {vr(inv)}, 0, {vr(inv)}, vcc")
         # rows of this query block that exist: exec = (qrow < q_end)
         skip = g.new_label("nostore")
         g(f"s_mov_b64 {sp(S_EXEC)}, exec")
-        g(f"v_cmp_gt_i32 vcc, %[qend], %[qrow{qb}]")
+        g(f"v_cmp_gt_i32 vcc, %[qend], {qrow}")
         g("s_and_b64 exec, exec, vcc")
         g(f"s_cbranch_execz {skip}")
         # output row address: obase + qrow * ldob + hh * 8 bytes (+ (d*32 + g*8) * 2)
         addr = S_SET[0]  # v[0:1] (S set A is dead here)
-        g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, %[qrow{qb}], %[ldob], 0")
+        g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {qrow}, %[ldob], 0")
         g(f"v_add_co_u32 {vr(addr)}, vcc, %[obase_lo], {vr(addr)}")
         g(f"v_mov_b32 {vr(addr + 2)}, %[obase_hi]")
         g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(addr + 2)}, {vr(addr + 1)}, vcc")
-        g(f"v_add_co_u32 {vr(addr)}, vcc, %[hh8], {vr(addr)}")
+        hh8 = opnd(g, "hh8", EPI_L + 5)
+        g(f"v_add_co_u32 {vr(addr)}, vcc, {hh8}, {vr(addr)}")
         g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
         for d in range(DT):
             for gg in range(4):
@@ -638,17 +730,18 @@ def epilogue(g):
         # lse = (m + log2 l) * ln 2 for lanes of the first half-wave, when asked
         g(f"s_cmp_eq_u32 %[has_lse], 0")
         g(f"s_cbranch_scc1 {skip}")
-        g(f"v_cmp_gt_u32 vcc, 32, %[lane]")
+        lane = opnd(g, "lane", EPI_L + 5)
+        g(f"v_cmp_gt_u32 vcc, 32, {lane}")
         g("s_and_b64 exec, exec, vcc")
         g(f"s_cbranch_execz {skip}")
         g(f"v_log_f32 {vr(12)}, {vr(lt)}")
         g("s_nop 0")
-        g(f"v_sub_f32 {vr(12)}, {vr(12)}, {vr(NEGM + qb)}")
+        g(f"v_sub_f32 {vr(12)}, {vr(12)}, {vr(negm(qb))}")
         g(f"v_mul_f32 {vr(12)}, 0x3f317218, {vr(12)}")
         g(f"v_cmp_lt_f32 vcc, 0, {vr(lt)}")
         g(f"v_mov_b32 {vr(14)}, 0xff800000")
         g(f"v_cndmask_b32 {vr(12)}, {vr(14)}, {vr(12)}, vcc")
-        g(f"v_lshlrev_b32 {vr(13)}, 2, %[qrow{qb}]")
+        g(f"v_lshlrev_b32 {vr(13)}, 2, {qrow}")
         g(f"global_store_dword {vr(13)}, {vr(12)}, %[lsebase]")
         g.label(skip)
         g(f"s_mov_b64 exec, {sp(S_EXEC)}")
@@ -656,7 +749,8 @@ def epilogue(g):
 
 def generate():
     g = Gen()
-    prologue(g)
+    empty = g.new_label("nokeys")
+    prologue(g, empty)
     last_a = g.new_label("lastA")
     last_b = g.new_label("lastB")
     loop = g.new_label("loop")
@@ -684,25 +778,32 @@ def generate():
     g(f"s_branch {fin}")
     g.label(last_b)
     last_tile(g, 1)
+    g(f"s_branch {fin}")
+    g.label(empty)
+    for i in range(2 * DT * 16):
+        g(f"v_accvgpr_write_b32 {ar(O_A + i)}, 0")
+    for qb in range(2):
+        g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
     g.label(fin)
     epilogue(g)
     return g.lines
 
 
-def clobbers(hd):
-    configure(hd)
+def clobbers(hd, pre=False):
+    configure(hd, pre)
     regs = ([f"v{i}" for i in range(LAST_VGPR + 1)] + [f"a{i}" for i in range(LAST_AGPR + 1)] +
             [f"s{i}" for i in SGPRS])
     rows = [", ".join(f'"{r}"' for r in regs[i:i + 16]) for i in range(0, len(regs), 16)]
-    return (f"// Registers the generated flash_fwd_asm<{hd}> body owns (gen_attn.py register map).\n"
-            f"#define DITK_D{hd}_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
+    name = f"{hd}{'p' if pre else ''}"
+    return (f"// Registers the generated flash_fwd_asm<{hd}, {str(pre).lower()}> body owns (gen_attn.py register map).\n"
+            f"#define DITK_D{name.upper()}_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
 
 
-def write_body(path, hd):
-    configure(hd)
+def write_body(path, hd, pre=False):
+    configure(hd, pre)
     lines = generate()
     with open(path, "w") as f:
-        f.write(f"// Generated by gen_attn.py -- the instruction body of flash_fwd_asm<{hd}>.\n")
+        f.write(f"// Generated by gen_attn.py -- the instruction body of flash_fwd_asm<{hd}, {str(pre).lower()}>.\n")
         for line in lines:
             esc = line.replace("\\", "\\\\").replace('"', '\\"')
             f.write(f'"{esc}\\n"\n')
@@ -712,9 +813,11 @@ def main(argv):
     here = os.path.dirname(os.path.abspath(__file__))
     out = os.path.dirname(os.path.abspath(argv[1])) if len(argv) > 1 else here
     for hd in (128, 64):
-        write_body(os.path.join(out, f"attn_d{hd}_body.inc"), hd)
-        with open(os.path.join(out, f"attn_d{hd}_clobbers.h"), "w") as f:
-            f.write(clobbers(hd))
+        for pre in (False, True):
+            name = f"d{hd}{'p' if pre else ''}"
+            write_body(os.path.join(out, f"attn_{name}_body.inc"), hd, pre)
+            with open(os.path.join(out, f"attn_{name}_clobbers.h"), "w") as f:
+                f.write(clobbers(hd, pre))
     return 0
 
 

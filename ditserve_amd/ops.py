@@ -303,9 +303,10 @@ def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None
 
     q [Tq, heads*head_dim], k/v [Tk, heads*head_dim] bf16 (row strides may
     differ, e.g. slices of a fused QKV buffer).  Returns out [Tq, heads*head_dim]
-    (and lse [heads, Tq] fp32, natural log, when return_lse).  q_prescaled
-    (head_dim 64): q already holds q * softmax_scale * log2(e), as a QK-norm
-    whose weight carries that factor produces it; softmax_scale must be None."""
+    (and lse [heads, Tq] fp32, natural log, when return_lse).  q_prescaled: q
+    already holds q * softmax_scale * log2(e), as a QK-norm whose weight carries
+    that factor produces it (the kernel then skips its per-score scaling);
+    softmax_scale must be None."""
     _check(q, "q", _BF16, 2)
     _check(k, "k", _BF16, 2)
     width = heads * head_dim

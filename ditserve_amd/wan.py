@@ -183,6 +183,11 @@ class WanTransformer:
         self.tx2_w, self.tx2_b = w(f"{ce}.text_embedder.linear_2.weight"), f(f"{ce}.text_embedder.linear_2.bias")
         self.sst_out = f("scale_shift_table").reshape(2, D)
         self.proj_w, self.proj_b = w("proj_out.weight"), f("proj_out.bias")
+        # The q RMSNorm weights (self and cross) carry softmax_scale * log2(e):
+        # the normed q leaves its norm kernel pre-scaled (still one bf16
+        # rounding) and attention starts its scores at -max with no per-score
+        # scaling.
+        q_mult = ops.LOG2E / math.sqrt(cfg.head_dim)
         self.blocks = []
         for i in range(cfg.layers):
             b = f"blocks.{i}"
@@ -191,13 +196,13 @@ class WanTransformer:
                 "sst": f(f"{b}.scale_shift_table").reshape(6, D),
                 "qkv_w": torch.cat([w(f"{a1}.to_q.weight"), w(f"{a1}.to_k.weight"), w(f"{a1}.to_v.weight")]),
                 "qkv_b": torch.cat([f(f"{a1}.to_q.bias"), f(f"{a1}.to_k.bias"), f(f"{a1}.to_v.bias")]),
-                "nq1": f(f"{a1}.norm_q.weight"), "nk1": f(f"{a1}.norm_k.weight"),
+                "nq1_pre": f(f"{a1}.norm_q.weight") * q_mult, "nk1": f(f"{a1}.norm_k.weight"),
                 "o1_w": w(f"{a1}.to_out.0.weight"), "o1_b": f(f"{a1}.to_out.0.bias"),
                 "n2_w": f(f"{b}.norm2.weight"), "n2_b": f(f"{b}.norm2.bias"),
                 "q2_w": w(f"{a2}.to_q.weight"), "q2_b": f(f"{a2}.to_q.bias"),
                 "kv2_w": torch.cat([w(f"{a2}.to_k.weight"), w(f"{a2}.to_v.weight")]),
                 "kv2_b": torch.cat([f(f"{a2}.to_k.bias"), f(f"{a2}.to_v.bias")]),
-                "nq2": f(f"{a2}.norm_q.weight"), "nk2": f(f"{a2}.norm_k.weight"),
+                "nq2_pre": f(f"{a2}.norm_q.weight") * q_mult, "nk2": f(f"{a2}.norm_k.weight"),
                 "o2_w": w(f"{a2}.to_out.0.weight"), "o2_b": f(f"{a2}.to_out.0.bias"),
                 "f1_w": w(f"{b}.ffn.net.0.proj.weight"), "f1_b": f(f"{b}.ffn.net.0.proj.bias"),
                 "f2_w": w(f"{b}.ffn.net.2.weight"), "f2_b": f(f"{b}.ffn.net.2.bias"),
@@ -323,11 +328,11 @@ class WanTransformer:
             qkv = ops.linear(x, blk["qkv_w"], blk["qkv_b"])
         q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
         with prof.region("qk_norm_rope"):
-            ops.qk_norm_rope_(q, k, blk["nq1"], blk["nk1"], Dh, cfg.eps, rope=packet["rotary"])
+            ops.qk_norm_rope_(q, k, blk["nq1_pre"], blk["nk1"], Dh, cfg.eps, rope=packet["rotary"])
         with prof.region("transpose_v"):
             vt = ops.transpose_v(v, H, Dh, seg)
         with prof.region("attn_self"):
-            a = ops.flash_attn_varlen(q, k, None, seg, seg, H, Dh, vt=vt)
+            a = ops.flash_attn_varlen(q, k, None, seg, seg, H, Dh, vt=vt, q_prescaled=True)
         with prof.region("gemm_o_gate"):
             h = ops.linear(a, blk["o1_w"], blk["o1_b"], "gate_res", residual=h, gate=mod[:, 2], segments=seg)
         # cross-attention (_stage2, block.py:288-290)
@@ -336,11 +341,11 @@ class WanTransformer:
             q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
             kv2 = ops.linear(packet["encoder"], blk["kv2_w"], blk["kv2_b"])
             k2, v2 = kv2[:, :D], kv2[:, D:]
-            ops.adaln(q2, weight=blk["nq2"], eps=cfg.eps, kind="rms", out=q2)
+            ops.adaln(q2, weight=blk["nq2_pre"], eps=cfg.eps, kind="rms", out=q2)
             ops.adaln(k2, weight=blk["nk2"], eps=cfg.eps, kind="rms", out=k2)
             vt2 = ops.transpose_v(v2, H, Dh, seg_txt)
         with prof.region("attn_cross"):
-            a = ops.flash_attn_varlen(q2, k2, None, seg, seg_txt, H, Dh, vt=vt2)
+            a = ops.flash_attn_varlen(q2, k2, None, seg, seg_txt, H, Dh, vt=vt2, q_prescaled=True)
         with prof.region("gemm_o_res"):
             ops.linear(a, blk["o2_w"], blk["o2_b"], "res", residual=h, out=h)
         # FFN (block.py:291-293)

@@ -106,12 +106,14 @@ int ditk_flash_attn_varlen(const void* q, int64_t ldq, const void* k, int64_t ld
 
 /*
  * ditk_flash_attn_varlen with q already multiplied by softmax_scale * log2(e)
- * (head_dim 64 only).  A producer that folds that factor into its QK-norm weight
- * still rounds q to bf16 once, and the kernel then starts its score accumulators
- * at -max and exponentiates them directly, one fused multiply-add per score fewer.
- * No reference counterpart: used by the SD3.5 joint and dual attention, which
- * replace the reference's SD3.5 varlen slot (sd35_batch.py:19-119,448-486) with
- * their per-head RMSNorm weight pre-multiplied.
+ * (head_dim 64 or 128).  A producer that folds that factor into its QK-norm
+ * weight still rounds q to bf16 once, and the kernel then starts its score
+ * accumulators at -max and exponentiates them directly, one fused multiply-add
+ * per score fewer.  No reference counterpart: used by the Wan self- and
+ * cross-attention (the q RMSNorm weights of transformer_wan.py:50-69 pre-
+ * multiplied) and the SD3.5 dual attention, which replaces the reference's SD3.5
+ * varlen slot (sd35_batch.py:19-119,448-486) with its per-head RMSNorm weight
+ * pre-multiplied.
  */
 int ditk_flash_attn_varlen_q_prescaled(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* vt,
                                        int64_t vt_ld, void* o, int64_t ldo, float* lse, int64_t lse_ld,

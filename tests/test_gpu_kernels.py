@@ -250,15 +250,17 @@ def test_attention_rising_scores(Dh):
     assert_close(out, _attn_ref(q, k, v, cu, cu, H, Dh), cos_min=0.9999, rel_max=1e-2, label=f"rising Dh={Dh}")
 
 
+@pytest.mark.parametrize("Dh", [128, 64])
 @pytest.mark.parametrize("case", ["random", "rising"])
 @pytest.mark.parametrize("lens", [[1], [64, 65], [300, 1, 129, 511], [1025]])
-def test_attention_q_prescaled(case, lens):
-    """head_dim 64 with q already multiplied by softmax_scale*log2(e): the kernel starts its
-    score accumulators at -max and must move them whenever the max rises (rising scores
-    force that in every tile).  Reference: the oracle on the same bf16 q' rescaled back by
-    ln 2 * sqrt(Dh) in fp32, so that its softmax(q.k / sqrt(Dh)) equals 2^(q'.k)."""
+def test_attention_q_prescaled(Dh, case, lens):
+    """q already multiplied by softmax_scale*log2(e): the kernel starts its score
+    accumulators at -max and must move them, and the next tile's already computed scores,
+    whenever the max rises (rising scores force that in every tile).  Reference: the oracle
+    on the same bf16 q' rescaled back by ln 2 * sqrt(Dh) in fp32, so that its
+    softmax(q.k / sqrt(Dh)) equals 2^(q'.k)."""
     ops = _ops()
-    H, Dh = 3, 64
+    H = 3
     cu = [0]
     for n in lens:
         cu.append(cu[-1] + n)
@@ -289,12 +291,26 @@ def test_attention_q_prescaled(case, lens):
         assert torch.allclose(lse[:, s0:s1].cpu(), ref_lse, atol=2e-3, rtol=1e-4)
 
 
-def test_attention_q_prescaled_rejects_head_dim_128():
+@pytest.mark.parametrize("Dh", [128, 64])
+@pytest.mark.parametrize("pre", [False, True])
+def test_attention_segments_without_keys(Dh, pre):
+    """A segment with no keys (first and last here, the last one starting at the end of
+    K) attends to nothing: zero output rows and lse = -inf; the others are unaffected."""
     ops = _ops()
-    x = torch.zeros((64, 128), dtype=torch.bfloat16, device=DEV)
-    seg = _seg([0, 64])
-    with pytest.raises(RuntimeError, match="head_dim must be 64"):
-        ops.flash_attn_varlen(x, x, x, seg, seg, 1, 128, q_prescaled=True)
+    H = 2
+    cu_q, cu_k = [0, 100, 300, 301], [0, 0, 130, 130]
+    q, k, v = _attn_case(cu_q, cu_k, H, Dh, 97)
+    qd = bf(q * (ops.LOG2E / math.sqrt(Dh))) if pre else q
+    out, lse = ops.flash_attn_varlen(qd.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16),
+                                     v.to(DEV, torch.bfloat16), _seg(cu_q), _seg(cu_k), H, Dh, return_lse=True,
+                                     q_prescaled=pre)
+    out, lse = out.float().cpu(), lse.cpu()
+    for s0, s1 in ((0, 100), (300, 301)):
+        assert torch.equal(out[s0:s1], torch.zeros_like(out[s0:s1]))
+        assert bool(torch.all(lse[:, s0:s1] == -math.inf))
+    q_ref = qd * (math.log(2.0) * math.sqrt(Dh)) if pre else q
+    ref = _attn_ref(q_ref[100:300], k, v, [0, 200], [0, 130], H, Dh)
+    assert_close(out[100:300], ref, cos_min=0.9999, rel_max=1e-2, label=f"no-keys neighbours Dh={Dh} pre={pre}")
 
 
 @pytest.mark.parametrize("Dh", [128, 64])

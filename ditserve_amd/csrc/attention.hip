@@ -713,6 +713,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [koffl0] "a"(koffl[0]), [koffl1] "a"(koffl[1]), [koffl2] "a"(koffl[2]), [koffl3] "a"(koffl[3]),             \
       [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
       [xaddr] "a"(xaddr), [hh8] "a"(hh8), [lane] "a"(lanev), [qrow0] "a"(qrow0), [qrow1] "a"(qrow1)
+constexpr int kXcdChunk = 32;  // work items per XCD chunk (one per CU of an XCD)
 template <int HD, bool PRE>
 __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
@@ -723,14 +724,30 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   constexpr int ND = HD / 32;  // DMA instructions per wave and operand per tile
   __shared__ u32x4_t Ks[2][BN * HD / 8];
   __shared__ u32x4_t Vs[2][HD * 8];
-  const int nb = gridDim.x;
+  // Work items in segment-major order (segment, then head, then 256-query tile),
+  // dealt to the 8 XCDs (workgroup b runs on XCD b % 8) in chunks of kXcdChunk
+  // consecutive items: every XCD gets every 8th chunk, so a ragged batch spreads
+  // evenly over the XCDs, and the items running on one XCD at a time are tiles of
+  // the same (segment, head), sharing its K and Vt in that XCD's L2.  The grid is
+  // a multiple of 8 chunks; items past the last tile exit at once.
   const int b = blockIdx.x;
-  const int logical = (b & 7) * (nb >> 3) + (b >> 3);
-  const int head = logical / tiles_bound;
-  int t = logical % tiles_bound;
-  if (head >= heads) return;
-  const int seg = locate_tile(cu_q, nseg, BM, t);
+  const int j = b >> 3;
+  int t = ((j / kXcdChunk) * 8 + (b & 7)) * kXcdChunk + j % kXcdChunk;
+  int seg = -1, head = 0;
+  for (int m = 0, prev = cu_q[0]; m < nseg; ++m) {
+    const int next = cu_q[m + 1];
+    const int n = (next - prev + BM - 1) / BM;
+    if (t < n * heads) {
+      seg = m;
+      head = t / n;
+      t -= head * n;
+      break;
+    }
+    t -= n * heads;
+    prev = next;
+  }
   if (seg < 0) return;
+  (void)tiles_bound;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -950,7 +967,7 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
                  "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
     const int tiles_bound = (Tq + 255) / 256 + nseg;
     int64_t nblocks = (int64_t)tiles_bound * heads;
-    nblocks = (nblocks + 7) / 8 * 8;
+    nblocks = (nblocks + 8 * kXcdChunk - 1) / (8 * kXcdChunk) * (8 * kXcdChunk);
     DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
     auto kern = head_dim == 128 ? (pre ? flash_fwd_asm<128, true> : flash_fwd_asm<128, false>)
                                 : (pre ? flash_fwd_asm<64, true> : flash_fwd_asm<64, false>);

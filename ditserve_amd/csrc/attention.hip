@@ -690,7 +690,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
-      [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),             \
+      [lds_o] "s"(su(lds_o)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),             \
       [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
       [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
       [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
@@ -705,7 +705,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
-      [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),                           \
+      [lds_o] "s"(su(lds_o)), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),                           \
       [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
       [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
       [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
@@ -724,6 +724,8 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   constexpr int ND = HD / 32;  // DMA instructions per wave and operand per tile
   __shared__ u32x4_t Ks[2][BN * HD / 8];
   __shared__ u32x4_t Vs[2][HD * 8];
+  constexpr int OPITCH = HD * 2 + 8;  // output staging row pitch (bytes), 32 rows per wave
+  __shared__ u32x4_t Os[4 * 32 * OPITCH / 16];
   // Work items in segment-major order (segment, then head, then 256-query tile),
   // dealt to the 8 XCDs (workgroup b runs on XCD b % 8) in chunks of kXcdChunk
   // consecutive items: every XCD gets every 8th chunk, so a ragged batch spreads
@@ -774,6 +776,8 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   // last row) and Vt DMA source offsets, per lane
   const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Ks[0][0];
   const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Vs[0][0];
+  const uint32_t lds_o = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)&Os[0] +
+                         (uint32_t)wave_u * (32 * OPITCH);
   uint32_t kaddr[4], vaddr[4], koff[4] = {}, koffl[4] = {}, voff[4] = {};
   const int lrow = lane >> 3;
   const int lsw0 = ((lane & 7) ^ ((lane >> 4) & 7)) * 8;

@@ -676,9 +676,33 @@ def prologue(g, empty):
 
 
 def epilogue(g):
-    """l total over both half-waves, O / l to bf16, stores; lse when asked."""
+    """l total over both half-waves, O / l to bf16, stores; lse when asked.
+
+    Each 32-query block goes through this wave's LDS staging rows (pitch HD * 2 +
+    8 bytes, query q at row q) so that the global stores write whole row
+    segments: a lane owns 4 consecutive dims of one query in the accumulators,
+    but stores 16 bytes of one row, HD / 8 lanes per row."""
     g.nops(20)
     T = EPI_T
+    pitch = HD * 2 + 8
+    lpr = HD // 8                  # lanes per output row (16 bytes each)
+    rpr = 64 // lpr                # rows per store instruction
+    addr, wa, ra, t0, left, ohi = S_SET[0], 2, 3, 49, 48, 50
+    data = 16                      # v16.. read-back rows (4 per read)
+    lane = opnd(g, "lane", EPI_L + 5)
+    # LDS write address: row lane % 32, + 8 bytes for the upper half-wave;
+    # read address: row lane / lpr, 16-byte column lane % lpr
+    g(f"v_and_b32 {vr(t0)}, 31, {lane}")
+    g(f"v_mul_u32_u24 {vr(wa)}, {pitch}, {vr(t0)}")
+    g(f"v_lshrrev_b32 {vr(t0)}, 5, {lane}")
+    g(f"v_lshl_add_u32 {vr(wa)}, {vr(t0)}, 3, {vr(wa)}")
+    g(f"v_add_u32 {vr(wa)}, %[lds_o], {vr(wa)}")
+    g(f"v_lshrrev_b32 {vr(t0)}, {lpr.bit_length() - 1}, {lane}")
+    g(f"v_mul_u32_u24 {vr(ra)}, {pitch}, {vr(t0)}")
+    g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
+    g(f"v_lshl_add_u32 {vr(ra)}, {vr(t0)}, 4, {vr(ra)}")
+    g(f"v_add_u32 {vr(ra)}, %[lds_o], {vr(ra)}")
+    g(f"s_lshl_b32 {s_(S_T1)}, %[ldob], {rpr.bit_length() - 1}")   # rpr rows of output
     for qb in range(2):
         lt, inv, t = EPI_L + 0, EPI_L + 1, EPI_L + 2
         xa = opnd(g, "xaddr", EPI_L + 3)
@@ -701,21 +725,8 @@ def epilogue(g):
         g(f"v_div_fixup_f32 {vr(inv)}, {vr(T + 3)}, {vr(lt)}, 1.0")
         g(f"v_cmp_lt_f32 vcc, 0, {vr(lt)}")
         g(f"v_cndmask_b32 {vr(inv)}, 0, {vr(inv)}, vcc")
-        # rows of this query block that exist: exec = (qrow < q_end)
-        skip = g.new_label("nostore")
-        g(f"s_mov_b64 {sp(S_EXEC)}, exec")
-        g(f"v_cmp_gt_i32 vcc, %[qend], {qrow}")
-        g("s_and_b64 exec, exec, vcc")
-        g(f"s_cbranch_execz {skip}")
-        # output row address: obase + qrow * ldob + hh * 8 bytes (+ (d*32 + g*8) * 2)
-        addr = S_SET[0]  # v[0:1] (S set A is dead here)
-        g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {qrow}, %[ldob], 0")
-        g(f"v_add_co_u32 {vr(addr)}, vcc, %[obase_lo], {vr(addr)}")
-        g(f"v_mov_b32 {vr(addr + 2)}, %[obase_hi]")
-        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(addr + 2)}, {vr(addr + 1)}, vcc")
-        hh8 = opnd(g, "hh8", EPI_L + 5)
-        g(f"v_add_co_u32 {vr(addr)}, vcc, {hh8}, {vr(addr)}")
-        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
+        # O / l -> bf16 into the staging rows (every lane; rows past the end are
+        # written but never stored)
         for d in range(DT):
             for gg in range(4):
                 w0, w1 = 4, 5
@@ -726,11 +737,42 @@ def epilogue(g):
                     g(f"v_mul_f32 {vr(8 + k)}, {vr(8 + k)}, {vr(inv)}")
                 g(f"v_cvt_pk_bf16_f32 {vr(w0)}, {vr(8)}, {vr(9)}")
                 g(f"v_cvt_pk_bf16_f32 {vr(w1)}, {vr(10)}, {vr(11)}")
-                g(f"global_store_dwordx2 {vr(addr, 2)}, {vr(w0, 2)}, off offset:{(d * 32 + gg * 8) * 2}")
+                g(f"ds_write_b64 {vr(wa)}, {vr(w0, 2)} offset:{(d * 32 + gg * 8) * 2}")
+        g("s_waitcnt lgkmcnt(0)")
+        for i in range(32 // rpr):
+            g(f"ds_read_b128 {vr(data + 4 * i, 4)}, {vr(ra)} offset:{i * rpr * pitch}")
+        # this lane's first output row (block start + lane / lpr), rows left in
+        # the segment, and its address: obase + row * ldob + (lane % lpr) * 16
+        g(f"v_and_b32 {vr(t0)}, 31, {lane}")
+        g(f"v_sub_u32 {vr(left)}, {qrow}, {vr(t0)}")
+        g(f"v_lshrrev_b32 {vr(t0)}, {lpr.bit_length() - 1}, {lane}")
+        g(f"v_add_u32 {vr(left)}, {vr(left)}, {vr(t0)}")
+        g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {vr(left)}, %[ldob], 0")
+        g(f"v_sub_u32 {vr(left)}, %[qend], {vr(left)}")
+        g(f"v_add_co_u32 {vr(addr)}, vcc, %[obase_lo], {vr(addr)}")
+        g(f"v_mov_b32 {vr(ohi)}, %[obase_hi]")
+        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(ohi)}, {vr(addr + 1)}, vcc")
+        g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
+        g(f"v_lshlrev_b32 {vr(t0)}, 4, {vr(t0)}")
+        g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(t0)}, {vr(addr)}")
+        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
+        g("s_waitcnt lgkmcnt(0)")
+        g(f"s_mov_b64 {sp(S_EXEC)}, exec")
+        for i in range(32 // rpr):
+            if i:
+                g(f"s_mov_b64 exec, {sp(S_EXEC)}")
+                g(f"v_add_co_u32 {vr(addr)}, vcc, {s_(S_T1)}, {vr(addr)}")
+                g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
+            g(f"v_cmp_lt_i32 vcc, {i * rpr}, {vr(left)}")
+            g("s_and_b64 exec, exec, vcc")
+            g(f"global_store_dwordx4 {vr(addr, 2)}, {vr(data + 4 * i, 4)}, off")
+        g(f"s_mov_b64 exec, {sp(S_EXEC)}")
         # lse = (m + log2 l) * ln 2 for lanes of the first half-wave, when asked
+        skip = g.new_label("nolse")
         g(f"s_cmp_eq_u32 %[has_lse], 0")
         g(f"s_cbranch_scc1 {skip}")
-        lane = opnd(g, "lane", EPI_L + 5)
+        g(f"v_cmp_gt_i32 vcc, %[qend], {qrow}")
+        g("s_and_b64 exec, exec, vcc")
         g(f"v_cmp_gt_u32 vcc, 32, {lane}")
         g("s_and_b64 exec, exec, vcc")
         g(f"s_cbranch_execz {skip}")

@@ -690,7 +690,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
-      [lds_o] "s"(su(lds_o)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),             \
+      [lds_o] "s"(su(lds_o)), [npass] "s"(su(npass)), [ldqb] "s"(su(ldqb)), [sc] "s"(sc), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),             \
       [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
       [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
       [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
@@ -705,7 +705,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_fwd_kernel(
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
-      [lds_o] "s"(su(lds_o)), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),                           \
+      [lds_o] "s"(su(lds_o)), [npass] "s"(su(npass)), [ldqb] "s"(su(ldqb)), [qend] "s"(su(q_end)), [ldob] "s"(su(ldob)), [obase_lo] "s"(su((uint32_t)obase)),                           \
       [obase_hi] "s"(su((uint32_t)(obase >> 32))), [has_lse] "s"(su(has_lse)), [lsebase] "s"(su64(lsebase)),      \
       [kaddr0] "v"(kaddr[0]), [kaddr1] "v"(kaddr[1]), [kaddr2] "v"(kaddr[2]), [kaddr3] "v"(kaddr[3]),             \
       [vaddr0] "v"(vaddr[0]), [vaddr1] "v"(vaddr[1]), [vaddr2] "v"(vaddr[2]), [vaddr3] "v"(vaddr[3]),             \
@@ -719,37 +719,40 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
     const bf16_t* __restrict__ Q, int64_t ldq, const bf16_t* __restrict__ Kp, int64_t ldk,
     const bf16_t* __restrict__ Vt, int64_t vt_ld, int64_t vt_hs, bf16_t* __restrict__ O, int64_t ldo,
     float* __restrict__ lse, int64_t lse_ld, const int32_t* __restrict__ cu_q,
-    const int32_t* __restrict__ cu_k, int nseg, int heads, int tiles_bound, float scale_log2) {
+    const int32_t* __restrict__ cu_k, int nseg, int heads, int np, float scale_log2) {
   constexpr int NW = 4, BM = 256;
   constexpr int ND = HD / 32;  // DMA instructions per wave and operand per tile
   __shared__ u32x4_t Ks[2][BN * HD / 8];
   __shared__ u32x4_t Vs[2][HD * 8];
   constexpr int OPITCH = HD * 2 + 8;  // output staging row pitch (bytes), 32 rows per wave
   __shared__ u32x4_t Os[4 * 32 * OPITCH / 16];
-  // Work items in segment-major order (segment, then head, then 256-query tile),
-  // dealt to the 8 XCDs (workgroup b runs on XCD b % 8) in chunks of kXcdChunk
-  // consecutive items: every XCD gets every 8th chunk, so a ragged batch spreads
-  // evenly over the XCDs, and the items running on one XCD at a time are tiles of
-  // the same (segment, head), sharing its K and Vt in that XCD's L2.  The grid is
-  // a multiple of 8 chunks; items past the last tile exit at once.
+  // A work item is np consecutive 256-query tiles of one (segment, head), run as
+  // passes of the body (the next pass's loads issued under the current pass's
+  // last key tile).  Items in segment-major order (segment, then head, then
+  // tile), dealt to the 8 XCDs (workgroup b runs on XCD b % 8) in chunks of
+  // kXcdChunk consecutive items: every XCD gets every 8th chunk, so a ragged
+  // batch spreads evenly over the XCDs, and the items running on one XCD at a
+  // time are tiles of the same (segment, head), sharing its K and Vt in that
+  // XCD's L2.  The grid is a multiple of 8 chunks; items past the last exit.
   const int b = blockIdx.x;
   const int j = b >> 3;
   int t = ((j / kXcdChunk) * 8 + (b & 7)) * kXcdChunk + j % kXcdChunk;
-  int seg = -1, head = 0;
+  int seg = -1, head = 0, npass = 0;
   for (int m = 0, prev = cu_q[0]; m < nseg; ++m) {
     const int next = cu_q[m + 1];
-    const int n = (next - prev + BM - 1) / BM;
+    const int ntile = (next - prev + BM - 1) / BM;
+    const int n = (ntile + np - 1) / np;
     if (t < n * heads) {
       seg = m;
       head = t / n;
-      t -= head * n;
+      t = (t - head * n) * np;
+      npass = min(np, ntile - t);
       break;
     }
     t -= n * heads;
     prev = next;
   }
   if (seg < 0) return;
-  (void)tiles_bound;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -803,6 +806,7 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   const uint32_t lanev = (uint32_t)lane;
   const uint64_t obase = (uint64_t)(uintptr_t)(O + (int64_t)head * HD);
   const uint32_t ldob = (uint32_t)(ldo * 2);
+  const uint32_t ldqb = (uint32_t)(ldq * 2);
   const uint64_t lsebase = (uint64_t)(uintptr_t)(lse != nullptr ? lse + (int64_t)head * lse_ld : lse);
   const uint32_t has_lse = lse != nullptr;
   // scalar operands: wave-uniform values, made SGPR-resident explicitly
@@ -969,7 +973,11 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
     // one wave per SIMD, 64 queries per wave: generated-assembly body
     DITK_REQUIRE((int64_t)Tq * ldq * 2 < (1ll << 32) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
                  "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
-    const int tiles_bound = (Tq + 255) / 256 + nseg;
+    // passes per work item: several query tiles per workgroup when the segments
+    // have few keys (vt_ld / nseg bounds the mean key count from above), so the
+    // next tile's loads hide under the current one's last key tile
+    const int np = vt_ld / nseg <= 2048 ? 4 : 1;
+    const int tiles_bound = ((Tq + 255) / 256 + nseg + np - 1) / np + nseg;
     int64_t nblocks = (int64_t)tiles_bound * heads;
     nblocks = (nblocks + 8 * kXcdChunk - 1) / (8 * kXcdChunk) * (8 * kXcdChunk);
     DITK_REQUIRE(nblocks < (1ll << 31), "ditk_flash_attn_varlen: grid too large");
@@ -977,7 +985,7 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
                                 : (pre ? flash_fwd_asm<64, true> : flash_fwd_asm<64, false>);
     kern<<<(unsigned)nblocks, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk, (const bf16_t*)vt,
                                                 vt_ld, hs, (bf16_t*)o, ldo, lse, lse_ld, cu_q, cu_k, nseg, heads,
-                                                tiles_bound, sl2);
+                                                np, sl2);
     rc = 0;
   }
   if (rc) return rc;

@@ -109,7 +109,9 @@ S_CMP = 70       # s[70:71] compare mask
 S_EXEC = 72      # s[72:73] saved exec
 S_VALID = 74     # s74 valid keys of the last tile
 S_THR = 75       # s75 the lazy-rescale threshold 256.0
-SGPRS = list(range(60, 76))
+S_QOFF = 76      # s76 query-row offset of the current pass (256 per pass)
+S_NPASS = 77     # s77 passes left, this one included
+SGPRS = list(range(60, 78))
 
 
 def s_(n):
@@ -564,6 +566,29 @@ def last_tile(g, a):
     checked = g.new_label("lastchecked")
     g.nops(20)
     g.lds_wait_all()
+    # another pass follows: its Q (into the Q AGPRs, free since this tile has no
+    # S MFMAs), K(0) and K(1) (no wave reads K any more: all passed the last
+    # tile barrier), and, when this tile's Vt is in stage 1, Vt(0) into stage 0
+    nopf = g.new_label("noprefetch")
+    g(f"s_cmp_gt_u32 {s_(S_NPASS)}, 1")
+    g(f"s_cbranch_scc0 {nopf}")
+    tmp = S_SET[1 - a]  # S set of the next tile: free in the last tile
+    g(f"s_add_u32 {s_(S_T0)}, {s_(S_QOFF)}, {BN * 4}")
+    g(f"s_sub_u32 {s_(S_T1)}, %[qend], 1")
+    hh8 = opnd(g, "hh8", tmp + 2)
+    g(f"v_lshlrev_b32 {vr(tmp + 2)}, 1, {hh8}")
+    for qb in range(2):
+        qrow = opnd(g, f"qrow{qb}", tmp + qb)
+        g(f"v_add_u32 {vr(tmp + qb)}, {s_(S_T0)}, {qrow}")
+        g(f"v_min_i32 {vr(tmp + qb)}, {s_(S_T1)}, {vr(tmp + qb)}")
+        g(f"v_mul_lo_u32 {vr(tmp + qb)}, {vr(tmp + qb)}, %[ldqb]")
+        g(f"v_add_u32 {vr(tmp + qb)}, {vr(tmp + qb)}, {vr(tmp + 2)}")
+        for c in range(NC):
+            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(tmp + qb)}, %[qbase] offset:{c * 32}")
+    first_k_dmas(g)
+    if a == 1:
+        first_vt_dma(g)
+    g.label(nopf)
     for qb in range(2):
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
     g(f"s_cmp_eq_u32 {s_(S_VALID)}, {BN}")
@@ -593,31 +618,21 @@ def last_tile(g, a):
     for f in range(4):
         v_read(g, f, a)
     o_phase(g, a, vstage=a, items=None)
+    # another pass: its loads landed and published, this tile's Vt reads done
+    # in every wave; then Vt(0) into stage 0 if this tile used it
+    nxt = g.new_label("lastdone")
+    g(f"s_cmp_gt_u32 {s_(S_NPASS)}, 1")
+    g(f"s_cbranch_scc0 {nxt}")
+    g("s_waitcnt vmcnt(0)")
+    g("s_barrier")
+    if a == 0:
+        first_vt_dma(g)
+    g.label(nxt)
 
 
-def prologue(g, empty):
-    """empty: the label of the no-keys exit (O = 0, l = 0: the epilogue then
-    stores zero rows and lse = -inf)."""
-    # scalar state
-    g(f"s_mov_b32 {s_(S_VDMA)}, %[vdma_lo]")
-    g(f"s_mov_b32 {s_(S_VDMA + 1)}, %[vdma_hi]")
-    g(f"s_add_u32 {s_(S_KW)}, %[lds_k], %[wave1k]")
-    g(f"s_add_u32 {s_(S_VW)}, %[lds_v], %[wave1k]")
-    g(f"s_mov_b32 {s_(S_KT)}, 0")
-    g(f"s_sub_u32 {s_(S_NKT1)}, %[nkt], 1")
-    g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
-    g(f"s_mov_b32 {s_(S_THR)}, 0x43800000")
-    g("s_cmp_eq_u32 %[nkt], 0")
-    g(f"s_cbranch_scc1 {empty}")
-    # Q fragments straight into AGPRs, then the DMAs of K(0) (K stage 0), K(1)
-    # (K stage 1; K(0) again when there is one tile) and Vt(0) (Vt stage 0), all
-    # before the first wait so that their latencies overlap
-    if PRE:
-        g("s_nop 4")  # the AGPR operands were written just before the body
-    for qb in range(2):
-        qo = opnd(g, f"qoff{qb}", S_SET[0] + qb)
-        for c in range(NC):
-            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {qo}, %[qbase] offset:{c * 32}")
+def first_k_dmas(g):
+    """DMA K(0) into K stage 0 and K(1) into stage 1 (K(0) again when there is
+    one tile), with the clamped offsets for whichever is the last tile."""
     for i in range(ND):
         if PRE:
             g(f"v_accvgpr_read_b32 {vr(KOFF + i)}, %[koff{i}]")
@@ -633,19 +648,62 @@ def prologue(g, empty):
     g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, 0")
     clamp_koff(g, f"s_cmp_le_u32 {s_(S_NKT1)}, 1")
     kdma_block(g, 1)
+
+
+def first_vt_dma(g):
+    """DMA Vt(0) into Vt stage 0; the Vt DMA base then points at tile 1."""
+    g(f"s_mov_b32 {s_(S_VDMA)}, %[vdma_lo]")
+    g(f"s_mov_b32 {s_(S_VDMA + 1)}, %[vdma_hi]")
     vdma_block(g, 0)
     g(f"s_add_u32 {s_(S_VDMA)}, {s_(S_VDMA)}, {BN * 2}")
     g(f"s_addc_u32 {s_(S_VDMA + 1)}, {s_(S_VDMA + 1)}, 0")
+
+
+def prologue(g, empty):
+    """The first pass's loads.  empty: the label of the no-keys path (O = 0,
+    l = 0: the epilogue then stores zero rows and lse = -inf)."""
+    # scalar state
+    g(f"s_mov_b32 {s_(S_QOFF)}, 0")
+    g(f"s_mov_b32 {s_(S_NPASS)}, %[npass]")
+    g(f"s_add_u32 {s_(S_KW)}, %[lds_k], %[wave1k]")
+    g(f"s_add_u32 {s_(S_VW)}, %[lds_v], %[wave1k]")
+    g(f"s_sub_u32 {s_(S_NKT1)}, %[nkt], 1")
+    g(f"s_mov_b32 {s_(S_VALID)}, %[valid_last]")
+    g(f"s_mov_b32 {s_(S_THR)}, 0x43800000")
+    g("s_cmp_eq_u32 %[nkt], 0")
+    g(f"s_cbranch_scc1 {empty}")
+    # Q fragments straight into AGPRs, then the DMAs of K(0) (K stage 0), K(1)
+    # (K stage 1; K(0) again when there is one tile) and Vt(0) (Vt stage 0), all
+    # before the first wait so that their latencies overlap
+    if PRE:
+        g("s_nop 4")  # the AGPR operands were written just before the body
+    for qb in range(2):
+        qo = opnd(g, f"qoff{qb}", S_SET[0] + qb)
+        for c in range(NC):
+            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {qo}, %[qbase] offset:{c * 32}")
+    first_k_dmas(g)
+    first_vt_dma(g)
     # O = 0, l = 0 while the loads fly
+    clear_state(g)
+    # Q and K(0) landed (the DMAs of K(1) and Vt(0) may still fly), K(0) published
+    g(f"s_waitcnt vmcnt({2 * ND})")
+    g("s_barrier")
+
+
+def clear_state(g):
+    """O = 0, l = 0, row sums 0, tile 0."""
     for i in range(2 * DT * 16):
         g(f"v_accvgpr_write_b32 {ar(O_A + i)}, 0")
     for qb in range(2):
         g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
         g(f"v_mov_b32 {vr(RS1 + qb)}, 0")
-    # Q and K(0) landed (the DMAs of K(1) and Vt(0) may still fly), K(0) published
-    g(f"s_waitcnt vmcnt({2 * ND})")
-    g("s_barrier")
+    g(f"s_mov_b32 {s_(S_KT)}, 0")
+
+
+def pass_start(g):
+    """S(0) of a pass (its Q, K(0) landed and published), the exact max of tile
+    0, then the wait for K(1) and Vt(0)."""
     # S(0) = K(0) Q^T into set A
     g.lds = []
     for c in range(2):
@@ -706,7 +764,8 @@ def epilogue(g):
     for qb in range(2):
         lt, inv, t = EPI_L + 0, EPI_L + 1, EPI_L + 2
         xa = opnd(g, "xaddr", EPI_L + 3)
-        qrow = opnd(g, f"qrow{qb}", EPI_L + 4)
+        qrow = vr(51)  # this lane's query row in this pass
+        g(f"v_add_u32 {qrow}, {s_(S_QOFF)}, {opnd(g, f'qrow{qb}', EPI_L + 4)}")
         g(f"ds_bpermute_b32 {vr(t)}, {xa}, {vr(LRUN + qb)}")
         g("s_waitcnt lgkmcnt(0)")
         g(f"v_add_f32 {vr(lt)}, {vr(LRUN + qb)}, {vr(t)}")
@@ -797,6 +856,10 @@ def generate():
     last_b = g.new_label("lastB")
     loop = g.new_label("loop")
     fin = g.new_label("fin")
+    npass = g.new_label("pass")
+    done = g.new_label("done")
+    g.label(npass)
+    pass_start(g)
     # P(0) keys 0..31 against the exact max (no check needed), only when a
     # steady tile follows
     g(f"s_cmp_le_u32 %[nkt], 1")
@@ -820,14 +883,28 @@ def generate():
     g(f"s_branch {fin}")
     g.label(last_b)
     last_tile(g, 1)
-    g(f"s_branch {fin}")
+    g.label(fin)
+    epilogue(g)
+    # next pass: 256 queries further, loads already issued by the last tile
+    g(f"s_sub_u32 {s_(S_NPASS)}, {s_(S_NPASS)}, 1")
+    g(f"s_cmp_eq_u32 {s_(S_NPASS)}, 0")
+    g(f"s_cbranch_scc1 {done}")
+    g(f"s_add_u32 {s_(S_QOFF)}, {s_(S_QOFF)}, {BN * 4}")
+    clear_state(g)
+    g(f"s_branch {npass}")
+    # no keys: every pass stores zero rows
     g.label(empty)
     for i in range(2 * DT * 16):
         g(f"v_accvgpr_write_b32 {ar(O_A + i)}, 0")
     for qb in range(2):
         g(f"v_mov_b32 {vr(LRUN + qb)}, 0")
-    g.label(fin)
     epilogue(g)
+    g(f"s_sub_u32 {s_(S_NPASS)}, {s_(S_NPASS)}, 1")
+    g(f"s_cmp_eq_u32 {s_(S_NPASS)}, 0")
+    g(f"s_cbranch_scc1 {done}")
+    g(f"s_add_u32 {s_(S_QOFF)}, {s_(S_QOFF)}, {BN * 4}")
+    g(f"s_branch {empty}")
+    g.label(done)
     return g.lines
 
 

@@ -40,9 +40,9 @@ GUIDANCE = 5.0
 SCHEDULE_STEPS = 50
 # HBM traffic of one headline self-attention launch, from two rocprofv3 --pmc passes
 # over this bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that
-# counter's reading for the CALIB_BYTES copy: FETCH 917547 KiB x 1.9998, WRITE
-# 196575 KiB x 1.0000 (profiles/wan21_480p_cfg2_step_traffic.md).
-ATTN_SELF_TRAFFIC_BYTES = (917547 * 1.9998 + 196575 * 1.0000) * 1024
+# counter's reading for the CALIB_BYTES copy: FETCH 884792 KiB x 1.9998, WRITE
+# 196560 KiB x 1.0000 (profiles/wan21_480p_cfg2_step_traffic.md).
+ATTN_SELF_TRAFFIC_BYTES = (884792 * 1.9998 + 196560 * 1.0000) * 1024
 
 WAN21_METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFMA peak"
 WORKLOADS = {
@@ -308,7 +308,7 @@ def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
         "tokens_per_step": 2 * seq, "blocks": cfg.layers,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-        "roofline": _roofline(f"flash_fwd_asm<128> (self-attention, 2 x {seq} tokens x {cfg.heads} heads)",
+        "roofline": _roofline(f"flash_fwd_asm<128, true> (self-attention, 2 x {seq} tokens x {cfg.heads} heads)",
                               attn_flops, regions["attn_self"],
                               ATTN_SELF_TRAFFIC_BYTES if name == "wan21_480p" else None,
                               4.0 * 2 * seq * cfg.dim * 2),
@@ -361,7 +361,7 @@ def run_wan_packed(steps, warmup, breakdown=False):
         "tokens_per_step": tokens, "blocks": cfg.layers,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-        "roofline": _roofline(f"flash_fwd_asm<128> (self-attention, 4 segments, {tokens} tokens x "
+        "roofline": _roofline(f"flash_fwd_asm<128, true> (self-attention, 4 segments, {tokens} tokens x "
                               f"{cfg.heads} heads)", attn_flops, regions["attn_self"],
                               algorithmic_bytes=4.0 * tokens * cfg.dim * 2),
         "reference_a100_ms_per_step": None, "vs_reference_a100": None,

@@ -975,8 +975,9 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
                  "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
     // passes per work item: several query tiles per workgroup when the segments
     // have few keys (vt_ld / nseg bounds the mean key count from above), so the
-    // next tile's loads hide under the current one's last key tile
-    const int np = vt_ld / nseg <= 2048 ? 4 : 1;
+    // next tile's loads hide under the current one's last key tile, as long as
+    // the items still fill the CUs at least twice over (512 items at 4 tiles each)
+    const int np = (vt_ld / nseg <= 2048 && (int64_t)((Tq + 255) / 256) * heads >= 2048) ? 4 : 1;
     const int tiles_bound = ((Tq + 255) / 256 + nseg + np - 1) / np + nseg;
     int64_t nblocks = (int64_t)tiles_bound * heads;
     nblocks = (nblocks + 8 * kXcdChunk - 1) / (8 * kXcdChunk) * (8 * kXcdChunk);

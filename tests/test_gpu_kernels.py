@@ -293,6 +293,44 @@ def test_attention_q_prescaled(Dh, case, lens):
 
 @pytest.mark.parametrize("Dh", [128, 64])
 @pytest.mark.parametrize("pre", [False, True])
+def test_attention_query_tile_passes_bitwise(Dh, pre):
+    """Short key ranges over many query tiles run several query tiles per workgroup, the
+    next tile's loads issued under the current one's last key tile.  With 16 heads the call
+    takes that path; one head at a time (too few tiles to fill the GPU that way) runs one
+    tile per workgroup: the outputs must be bitwise equal.  Segments: 65 query tiles (the
+    last work item one pass short) over 5 key tiles, 64 over 2, and 2 over none; sampled
+    rows are checked against the oracle."""
+    ops = _ops()
+    H = 16
+    cu_q, cu_k = [0, 16484, 32768, 33280], [0, 300, 377, 377]
+    g = torch.Generator(device=DEV).manual_seed(98)
+    q = torch.randn((cu_q[-1], H * Dh), generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn((cu_k[-1], H * Dh), generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn((cu_k[-1], H * Dh), generator=g, device=DEV).to(torch.bfloat16)
+    if pre:
+        q = (q.float() * (ops.LOG2E / math.sqrt(Dh))).to(torch.bfloat16)
+    sq, sk = _seg(cu_q), _seg(cu_k)
+    full, lse = ops.flash_attn_varlen(q, k, v, sq, sk, H, Dh, return_lse=True, q_prescaled=pre)
+    for h in range(H):
+        cols = slice(h * Dh, (h + 1) * Dh)
+        one, lse1 = ops.flash_attn_varlen(q[:, cols], k[:, cols], v[:, cols], sq, sk, 1, Dh, return_lse=True,
+                                          q_prescaled=pre)
+        assert torch.equal(one, full[:, cols]), f"head {h}"
+        assert torch.equal(lse1[0], lse[h]), f"lse head {h}"
+    rows = torch.tensor([0, 255, 256, 16383, 16483, 16484, 16740, 32767], device=DEV)
+    qs = q[rows].float().cpu()
+    q_ref = qs * (math.log(2.0) * math.sqrt(Dh)) if pre else qs
+    for i, r in enumerate(rows.tolist()):
+        m = 0 if r < cu_q[1] else 1
+        ref = _attn_ref(q_ref[i:i + 1], k[cu_k[m]:cu_k[m + 1]].float().cpu(), v[cu_k[m]:cu_k[m + 1]].float().cpu(),
+                        [0, 1], [0, cu_k[m + 1] - cu_k[m]], H, Dh)
+        assert_close(full[r:r + 1].float().cpu(), ref, cos_min=0.999, rel_max=1e-2, label=f"row {r}")
+    assert torch.equal(full[32768:], torch.zeros_like(full[32768:]))
+    assert bool(torch.all(lse[:, 32768:] == -math.inf))
+
+
+@pytest.mark.parametrize("Dh", [128, 64])
+@pytest.mark.parametrize("pre", [False, True])
 def test_attention_segments_without_keys(Dh, pre):
     """A segment with no keys (first and last here, the last one starting at the end of
     K) attends to nothing: zero output rows and lse = -inf; the others are unaffected."""

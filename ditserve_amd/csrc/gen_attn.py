@@ -739,7 +739,8 @@ def epilogue(g):
     Each 32-query block goes through this wave's LDS staging rows (pitch HD * 2 +
     8 bytes, query q at row q) so that the global stores write whole row
     segments: a lane owns 4 consecutive dims of one query in the accumulators,
-    but stores 16 bytes of one row, HD / 8 lanes per row."""
+    but stores 16 bytes of one row, HD / 8 lanes per row.  The stores are
+    non-temporal: nothing in the kernel reads the output again."""
     g.nops(20)
     T = EPI_T
     pitch = HD * 2 + 8
@@ -824,7 +825,7 @@ def epilogue(g):
                 g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
             g(f"v_cmp_lt_i32 vcc, {i * rpr}, {vr(left)}")
             g("s_and_b64 exec, exec, vcc")
-            g(f"global_store_dwordx4 {vr(addr, 2)}, {vr(data + 4 * i, 4)}, off")
+            g(f"global_store_dwordx4 {vr(addr, 2)}, {vr(data + 4 * i, 4)}, off nt")  # streamed
         g(f"s_mov_b64 exec, {sp(S_EXEC)}")
         # lse = (m + log2 l) * ln 2 for lanes of the first half-wave, when asked
         skip = g.new_label("nolse")

@@ -413,7 +413,7 @@ def run_sd35(steps, warmup, breakdown=False):
         "tokens_per_step": 2 * n_joint, "blocks": cfg.layers,
         "model_tflops": total_flops / (ms * 1e-3) / 1e12,
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-        "roofline": _roofline(f"flash_fwd_kernel<64> (joint attention, 2 x {n_joint} tokens x {cfg.heads} heads)",
+        "roofline": _roofline(f"flash_fwd_asm<64, true, true> (joint attention, 2 x {n_joint} tokens x {cfg.heads} heads)",
                               attn_flops, regions["attn_joint"], algorithmic_bytes=4.0 * 2 * n_joint * cfg.dim * 2),
         "reference_a100_ms_per_step": wl["ref_ms"], "vs_reference_a100": wl["ref_ms"] / ms,
         "_n_img": n_img, "_cfg": cfg,

@@ -35,16 +35,17 @@ Per 64-key tile kt the wave (queries q0..q0+63 of one (segment, head)) runs
 with one VALU half-item per MFMA slot, K fragments read two chunks ahead and
 Vt fragments four fragments ahead, and the next tiles' K and Vt streamed into
 LDS by direct global->LDS DMA.  The arithmetic per score, the order of every
-row sum and the rescale rule are those of the C++ kernel
-(flash_fwd_kernel<128, 8, 1>), so the two agree bitwise.
+row sum and the rescale rule are those of the compiler-scheduled C++ kernel
+this body replaced (8 waves of 32 queries), which it matched bitwise wherever
+no rescale fired.
 
 Hazards the hardware does not interlock are covered explicitly: an s_nop before
 VALU reads of MFMA results and before MFMAs read AGPRs written by
 v_accvgpr_write, an s_nop between an M0 write and the DMA that reads it.
 
-Usage: python gen_attn.py [dir/any]  (writes attn_d128_body.inc, attn_d128_clobbers.h,
-attn_d64_body.inc and attn_d64_clobbers.h into that directory, default beside
-this file)
+Usage: python gen_attn.py [dir/any]  (writes attn_d128_body.inc, attn_d128p_body.inc,
+attn_d64_body.inc, attn_d64p_body.inc, attn_d64j_body.inc and their
+*_clobbers.h into that directory, default beside this file)
 """
 import os
 import sys
@@ -57,7 +58,7 @@ VRING = 6        # Vt fragment ring (read four fragments ahead)
 BN = 64
 
 
-def configure(hd, pre=False):
+def configure(hd, pre=False, joint=False):
     """Head dim 128 or 64: NC 16-wide chunks of the head dim (K fragments per key
     half), DT 32-row d tiles of O^T, NF Vt fragments per tile (4 key groups x DT),
     ND DMA instructions per wave and operand per tile; AGPRs: O^T, then Q, the K
@@ -69,10 +70,20 @@ def configure(hd, pre=False):
     P = exp2(S) needs no per-score fma.  The VGPRs for the blocks come from a
     two-pair exp ring with the tile temporaries above it, no separate -m
     registers, and the per-lane operands used only outside the loop (Q and K DMA
-    offsets, output rows, lane constants) passed in AGPRs."""
+    offsets, output rows, lane constants) passed in AGPRs.
+
+    joint (with pre): a segment's rows are the rows of one segment of an "image"
+    source followed by those of a "text" source (SD3.5's joint attention).  A key
+    tile wholly in one source is DMA'd from that source's base with the usual
+    lane offsets; the one tile per segment across the seam is DMA'd at the tile
+    start in two lane-masked rounds (the slotted DMAs of that tile run with an
+    empty exec mask).  Q rows are loaded through per-lane 64-bit addresses and
+    output rows stored to the source they belong to.  Vt comes in the joint
+    layout.  One query tile per work item."""
     global HD, NC, DT, NF, ND, KSTAGE_BYTES, VSTAGE_BYTES, O_A, Q_A, KF_A, VF_A, LAST_AGPR
-    global PRE, TMP, RING, DTMP, RS0, RS1, NEGM, NEGB, LRUN, KOFF, LAST_VGPR, EPI_T, EPI_L
-    HD, PRE = hd, pre
+    global PRE, TMP, RING, DTMP, RS0, RS1, NEGM, NEGB, LRUN, KOFF, LAST_VGPR, EPI_T, EPI_L, JOINT
+    assert pre or not joint
+    HD, PRE, JOINT = hd, pre, joint
     TMP = 192
     if pre:
         RING, DTMP = 2, 196
@@ -111,7 +122,10 @@ S_VALID = 74     # s74 valid keys of the last tile
 S_THR = 75       # s75 the lazy-rescale threshold 256.0
 S_QOFF = 76      # s76 query-row offset of the current pass (256 per pass)
 S_NPASS = 77     # s77 passes left, this one included
+S_KEXEC = 78     # s[78:79] joint: exec mask of the slotted K DMAs of this tile
+S_KB2 = 80       # s[80:81] joint: the text source's K DMA base of the target tile
 SGPRS = list(range(60, 78))
+SGPRS_JOINT = list(range(60, 82))
 
 
 def s_(n):
@@ -266,7 +280,46 @@ def kdma_m0(g, i, stage):
 
 
 def kdma_go(g, i):
-    g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KDMA)}")
+    if JOINT:
+        g(f"s_mov_b64 exec, {sp(S_KEXEC)}")
+        g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KDMA)}")
+        g("s_mov_b64 exec, -1")
+    else:
+        g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KDMA)}")
+
+
+def joint_k_bases(g):
+    """Joint: K DMA bases of target tile T = S_T0 in both sources (S_KDMA: image,
+    S_KB2: text, each shifted so that lane offsets of tile rows apply) and S_T1 =
+    image rows of the segment from the tile's first row on (len_img - 64 T)."""
+    g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
+    g(f"s_mul_hi_u32 {s_(S_KDMA + 1)}, {s_(S_T0)}, %[ktile]")
+    g(f"s_add_u32 {s_(S_KB2)}, {s_(S_KDMA)}, %[ktxt_lo]")
+    g(f"s_addc_u32 {s_(S_KB2 + 1)}, {s_(S_KDMA + 1)}, %[ktxt_hi]")
+    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
+    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
+    g(f"s_lshl_b32 {s_(S_T1)}, {s_(S_T0)}, 6")
+    g(f"s_sub_i32 {s_(S_T1)}, %[lena], {s_(S_T1)}")
+
+
+def joint_k_dma_now(g, stage, tmp):
+    """Joint: DMA target tile T = S_T0 (bases from joint_k_bases, KOFF already
+    the clamped offsets if T is the last tile) into K stage `stage` now, in two
+    lane-masked rounds: lanes whose row (clamped like their offset) is an image
+    row, then the rest from the text source.  tmp: a free VGPR."""
+    g(f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
+    g(f"s_cselect_b32 {s_(S_CMP)}, {s_(S_VALID)}, {BN}")
+    g(f"s_sub_u32 {s_(S_CMP)}, {s_(S_CMP)}, 1")
+    for i in range(ND):
+        g(f"v_accvgpr_read_b32 {vr(tmp)}, %[krow{i}]")
+        g(f"v_min_u32 {vr(tmp)}, {s_(S_CMP)}, {vr(tmp)}")
+        g(f"v_cmp_gt_i32 vcc, {s_(S_T1)}, {vr(tmp)}")
+        kdma_m0(g, i, stage)
+        g("s_mov_b64 exec, vcc")
+        g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KDMA)}")
+        g("s_not_b64 exec, vcc")
+        g(f"global_load_lds_dwordx4 {vr(KOFF + i)}, {sp(S_KB2)}")
+        g("s_mov_b64 exec, -1")
 
 
 def vdma_m0(g, i, stage):
@@ -507,11 +560,28 @@ def tile(g, a):
     # K DMA source of tile min(kt+2, nkt-1); the last tile's rows past the end clamp
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_KT)}, 2")
     g(f"s_min_u32 {s_(S_T0)}, {s_(S_T0)}, {s_(S_NKT1)}")
-    g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
-    g(f"s_mul_hi_u32 {s_(S_KDMA + 1)}, {s_(S_T0)}, %[ktile]")
-    g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
-    g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
-    clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
+    if JOINT:
+        clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
+        joint_k_bases(g)
+        # wholly image: slotted DMAs from the image base; wholly text: from the
+        # text base; across the seam: DMA'd here, slotted DMAs masked off
+        kdone = g.new_label("kbase")
+        g(f"s_mov_b64 {sp(S_KEXEC)}, -1")
+        g(f"s_cmp_ge_i32 {s_(S_T1)}, {BN}")
+        g(f"s_cbranch_scc1 {kdone}")
+        g(f"s_mov_b64 {sp(S_KDMA)}, {sp(S_KB2)}")
+        g(f"s_cmp_le_i32 {s_(S_T1)}, 0")
+        g(f"s_cbranch_scc1 {kdone}")
+        g(f"s_mov_b64 {sp(S_KEXEC)}, 0")
+        joint_k_bases(g)
+        joint_k_dma_now(g, a, S_SET[b])
+        g.label(kdone)
+    else:
+        g(f"s_mul_i32 {s_(S_KDMA)}, {s_(S_T0)}, %[ktile]")
+        g(f"s_mul_hi_u32 {s_(S_KDMA + 1)}, {s_(S_T0)}, %[ktile]")
+        g(f"s_add_u32 {s_(S_KDMA)}, {s_(S_KDMA)}, %[kdma_lo]")
+        g(f"s_addc_u32 {s_(S_KDMA + 1)}, {s_(S_KDMA + 1)}, %[kdma_hi]")
+        clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
     dmas = ([(lambda i=i: kdma_m0(g, i, a), lambda i=i: kdma_go(g, i)) for i in range(ND)] +
             [(lambda i=i: vdma_m0(g, i, b), lambda i=i: vdma_go(g, i)) for i in range(ND)])
     # phase 1: S(kt+1) into set b || P(kt) keys 32..63 from set a
@@ -556,20 +626,9 @@ def rescale_block(g, a, resc, back):
     g(f"s_branch {back}")
 
 
-def last_tile(g, a):
-    """The last key tile (kt % 2 == a, scores in set a): P of all 64 keys against
-    m with keys past the segment end out of the row sums, the rescale test, then
-    O += Vt P."""
-    full = g.new_label("fullrs")
-    done_rs = g.new_label("rsdone")
-    resc = g.new_label("lastresc")
-    checked = g.new_label("lastchecked")
-    g.nops(20)
-    g.lds_wait_all()
-    # another pass follows: its Q (into the Q AGPRs, free since this tile has no
-    # S MFMAs), K(0) and K(1) (no wave reads K any more: all passed the last
-    # tile barrier), and, when this tile's Vt is in stage 1, Vt(0) into stage 0
-    nopf = g.new_label("noprefetch")
+def last_tile_prefetch(g, a, nopf):
+    """Under the last key tile of a pass with another pass to follow: that pass's
+    Q loads, K(0)/K(1) DMAs and (Vt of this tile in stage 1) its Vt(0) DMA."""
     g(f"s_cmp_gt_u32 {s_(S_NPASS)}, 1")
     g(f"s_cbranch_scc0 {nopf}")
     tmp = S_SET[1 - a]  # S set of the next tile: free in the last tile
@@ -588,6 +647,25 @@ def last_tile(g, a):
     first_k_dmas(g)
     if a == 1:
         first_vt_dma(g)
+
+
+def last_tile(g, a):
+    """The last key tile (kt % 2 == a, scores in set a): P of all 64 keys against
+    m with keys past the segment end out of the row sums, the rescale test, then
+    O += Vt P."""
+    full = g.new_label("fullrs")
+    done_rs = g.new_label("rsdone")
+    resc = g.new_label("lastresc")
+    checked = g.new_label("lastchecked")
+    g.nops(20)
+    g.lds_wait_all()
+    # another pass follows: its Q (into the Q AGPRs, free since this tile has no
+    # S MFMAs), K(0) and K(1) (no wave reads K any more: all passed the last
+    # tile barrier), and, when this tile's Vt is in stage 1, Vt(0) into stage 0
+    nopf = g.new_label("noprefetch")
+    multi = not JOINT  # joint work items are one query tile (one pass)
+    if multi:
+        last_tile_prefetch(g, a, nopf)
     g.label(nopf)
     for qb in range(2):
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
@@ -620,19 +698,29 @@ def last_tile(g, a):
     o_phase(g, a, vstage=a, items=None)
     # another pass: its loads landed and published, this tile's Vt reads done
     # in every wave; then Vt(0) into stage 0 if this tile used it
-    nxt = g.new_label("lastdone")
-    g(f"s_cmp_gt_u32 {s_(S_NPASS)}, 1")
-    g(f"s_cbranch_scc0 {nxt}")
-    g("s_waitcnt vmcnt(0)")
-    g("s_barrier")
-    if a == 0:
-        first_vt_dma(g)
-    g.label(nxt)
+    if multi:
+        nxt = g.new_label("lastdone")
+        g(f"s_cmp_gt_u32 {s_(S_NPASS)}, 1")
+        g(f"s_cbranch_scc0 {nxt}")
+        g("s_waitcnt vmcnt(0)")
+        g("s_barrier")
+        if a == 0:
+            first_vt_dma(g)
+        g.label(nxt)
 
 
 def first_k_dmas(g):
     """DMA K(0) into K stage 0 and K(1) into stage 1 (K(0) again when there is
     one tile), with the clamped offsets for whichever is the last tile."""
+    if JOINT:
+        for i in range(ND):
+            g(f"v_accvgpr_read_b32 {vr(KOFF + i)}, %[koff{i}]")
+        for t in range(2):
+            g(f"s_min_u32 {s_(S_T0)}, {t}, {s_(S_NKT1)}")
+            clamp_koff(g, f"s_cmp_eq_u32 {s_(S_T0)}, {s_(S_NKT1)}")
+            joint_k_bases(g)
+            joint_k_dma_now(g, t, S_SET[1])
+        return
     for i in range(ND):
         if PRE:
             g(f"v_accvgpr_read_b32 {vr(KOFF + i)}, %[koff{i}]")
@@ -678,6 +766,13 @@ def prologue(g, empty):
     if PRE:
         g("s_nop 4")  # the AGPR operands were written just before the body
     for qb in range(2):
+        if JOINT:  # per-lane 64-bit row address in its source
+            qa = S_SET[0] + 2 * qb
+            g(f"v_accvgpr_read_b32 {vr(qa)}, %[qa{qb}lo]")
+            g(f"v_accvgpr_read_b32 {vr(qa + 1)}, %[qa{qb}hi]")
+            for c in range(NC):
+                g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(qa, 2)}, off offset:{c * 32}")
+            continue
         qo = opnd(g, f"qoff{qb}", S_SET[0] + qb)
         for c in range(NC):
             g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {qo}, %[qbase] offset:{c * 32}")
@@ -807,19 +902,44 @@ def epilogue(g):
         g(f"v_sub_u32 {vr(left)}, {qrow}, {vr(t0)}")
         g(f"v_lshrrev_b32 {vr(t0)}, {lpr.bit_length() - 1}, {lane}")
         g(f"v_add_u32 {vr(left)}, {vr(left)}, {vr(t0)}")
-        g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {vr(left)}, %[ldob], 0")
+        if JOINT:
+            # row j of the segment (j0 + i * rpr for store i) goes to the image
+            # output while j < len_img, else to the text output; jbase[01] hold
+            # the two sources' segment bases (shifted by len_img for text) plus
+            # this lane's 16-byte column
+            j0, ib, tb = 52, 53, 55
+            g(f"v_subrev_u32 {vr(j0)}, %[qseg], {vr(left)}")
+            g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
+            g(f"v_lshlrev_b32 {vr(t0)}, 4, {vr(t0)}")
+            for base, src in ((ib, "oimg"), (tb, "otxt")):
+                g(f"v_mov_b32 {vr(base + 1)}, %[{src}_hi]")
+                g(f"v_add_co_u32 {vr(base)}, vcc, %[{src}_lo], {vr(t0)}")
+                g(f"v_addc_co_u32 {vr(base + 1)}, vcc, 0, {vr(base + 1)}, vcc")
+        else:
+            g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {vr(left)}, %[ldob], 0")
         g(f"v_sub_u32 {vr(left)}, %[qend], {vr(left)}")
-        g(f"v_add_co_u32 {vr(addr)}, vcc, %[obase_lo], {vr(addr)}")
-        g(f"v_mov_b32 {vr(ohi)}, %[obase_hi]")
-        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(ohi)}, {vr(addr + 1)}, vcc")
-        g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
-        g(f"v_lshlrev_b32 {vr(t0)}, 4, {vr(t0)}")
-        g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(t0)}, {vr(addr)}")
-        g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
+        if not JOINT:
+            g(f"v_add_co_u32 {vr(addr)}, vcc, %[obase_lo], {vr(addr)}")
+            g(f"v_mov_b32 {vr(ohi)}, %[obase_hi]")
+            g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(ohi)}, {vr(addr + 1)}, vcc")
+            g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
+            g(f"v_lshlrev_b32 {vr(t0)}, 4, {vr(t0)}")
+            g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(t0)}, {vr(addr)}")
+            g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
         g("s_waitcnt lgkmcnt(0)")
         g(f"s_mov_b64 {sp(S_EXEC)}, exec")
         for i in range(32 // rpr):
-            if i:
+            if JOINT:
+                if i:
+                    g(f"s_mov_b64 exec, {sp(S_EXEC)}")
+                    g(f"v_add_u32 {vr(j0)}, {rpr}, {vr(j0)}")
+                g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {vr(j0)}, %[ldob], 0")
+                g(f"v_cmp_gt_i32 vcc, %[lena], {vr(j0)}")
+                g(f"v_cndmask_b32 {vr(57)}, {vr(tb)}, {vr(ib)}, vcc")
+                g(f"v_cndmask_b32 {vr(58)}, {vr(tb + 1)}, {vr(ib + 1)}, vcc")
+                g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(57)}, {vr(addr)}")
+                g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(58)}, {vr(addr + 1)}, vcc")
+            elif i:
                 g(f"s_mov_b64 exec, {sp(S_EXEC)}")
                 g(f"v_add_co_u32 {vr(addr)}, vcc, {s_(S_T1)}, {vr(addr)}")
                 g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, 0, {vr(addr + 1)}, vcc")
@@ -909,21 +1029,22 @@ def generate():
     return g.lines
 
 
-def clobbers(hd, pre=False):
-    configure(hd, pre)
+def clobbers(hd, pre=False, joint=False):
+    configure(hd, pre, joint)
     regs = ([f"v{i}" for i in range(LAST_VGPR + 1)] + [f"a{i}" for i in range(LAST_AGPR + 1)] +
-            [f"s{i}" for i in SGPRS])
+            [f"s{i}" for i in (SGPRS_JOINT if joint else SGPRS)])
     rows = [", ".join(f'"{r}"' for r in regs[i:i + 16]) for i in range(0, len(regs), 16)]
-    name = f"{hd}{'p' if pre else ''}"
-    return (f"// Registers the generated flash_fwd_asm<{hd}, {str(pre).lower()}> body owns (gen_attn.py register map).\n"
+    name = f"{hd}{'j' if joint else 'p' if pre else ''}"
+    return (f"// Registers the generated flash_fwd_asm<{hd}, {str(pre).lower()}, {str(joint).lower()}> body owns (gen_attn.py register map).\n"
             f"#define DITK_D{name.upper()}_CLOBBERS \\\n" + "".join(f"  {r}, \\\n" for r in rows) + "\n")
 
 
-def write_body(path, hd, pre=False):
-    configure(hd, pre)
+def write_body(path, hd, pre=False, joint=False):
+    configure(hd, pre, joint)
     lines = generate()
     with open(path, "w") as f:
-        f.write(f"// Generated by gen_attn.py -- the instruction body of flash_fwd_asm<{hd}, {str(pre).lower()}>.\n")
+        f.write(f"// Generated by gen_attn.py -- the instruction body of flash_fwd_asm<{hd}, {str(pre).lower()}, "
+                f"{str(joint).lower()}>.\n")
         for line in lines:
             esc = line.replace("\\", "\\\\").replace('"', '\\"')
             f.write(f'"{esc}\\n"\n')
@@ -932,12 +1053,12 @@ def write_body(path, hd, pre=False):
 def main(argv):
     here = os.path.dirname(os.path.abspath(__file__))
     out = os.path.dirname(os.path.abspath(argv[1])) if len(argv) > 1 else here
-    for hd in (128, 64):
-        for pre in (False, True):
-            name = f"d{hd}{'p' if pre else ''}"
-            write_body(os.path.join(out, f"attn_{name}_body.inc"), hd, pre)
-            with open(os.path.join(out, f"attn_{name}_clobbers.h"), "w") as f:
-                f.write(clobbers(hd, pre))
+    for hd, pre, joint in ((128, False, False), (128, True, False), (64, False, False), (64, True, False),
+                           (64, True, True)):
+        name = f"d{hd}{'j' if joint else 'p' if pre else ''}"
+        write_body(os.path.join(out, f"attn_{name}_body.inc"), hd, pre, joint)
+        with open(os.path.join(out, f"attn_{name}_clobbers.h"), "w") as f:
+            f.write(clobbers(hd, pre, joint))
     return 0
 
 

@@ -507,6 +507,10 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
     }
   }
   constexpr int RB = HAS_RES ? NPASS : 1;  // every residual row loaded before the passes
+  // row pointers advanced by RPP rows per pass (no per-pass 64-bit multiplies)
+  const bf16_t* rrow = HAS_RES ? R + (int64_t)mrow * ldr + n : nullptr;
+  bf16_t* crow = reinterpret_cast<bf16_t*>(Cv) + (int64_t)mrow * ldc + n;
+  const int64_t rstep = (int64_t)RPP * ldr, cstep = (int64_t)RPP * ldc;
 #pragma unroll
   for (int r0 = 0; r0 < NPASS; r0 += RB) {
     u32x4_t res[RB];
@@ -515,7 +519,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
       for (int q = 0; q < RB; ++q) {
         const int m = mrow + (r0 + q) * RPP;
         const bool in = m < M && (r0 + q) * RPP + lane / CPR < WTM;
-        res[q] = in ? *reinterpret_cast<const u32x4_t*>(R + (int64_t)m * ldr + n) : u32x4_t{0, 0, 0, 0};
+        res[q] = in ? *reinterpret_cast<const u32x4_t*>(rrow) : u32x4_t{0, 0, 0, 0};
+        rrow += rstep;
       }
     }
 #pragma unroll
@@ -523,6 +528,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
       const int r = r0 + q;
       const int t = r * RPP + lane / CPR;
       const int m = mrow + r * RPP;
+      bf16_t* cp = crow;
+      crow += cstep;
       if (m >= M || t >= WTM) continue;
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + t * STG_ROW + c8 * 16);
       if (EPI != EPI_BIAS) {
@@ -556,7 +563,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
         }
         v = pack8(x);
       }
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(Cv) + (int64_t)m * ldc + n));
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(cp));
     }
   }
 }

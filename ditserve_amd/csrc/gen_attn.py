@@ -828,8 +828,9 @@ def pass_start(g):
         k_read(g, c, 1, 1)
 
 
-def epilogue(g):
-    """l total over both half-waves, O / l to bf16, stores; lse when asked.
+def epilogue(g, negm_of=None):
+    """l total over both half-waves, O / l to bf16, stores; lse when asked
+    (negm_of(qb): the register holding -m of query block qb, default negm).
 
     Each 32-query block goes through this wave's LDS staging rows (pitch HD * 2 +
     8 bytes, query q at row q) so that the global stores write whole row
@@ -838,11 +839,16 @@ def epilogue(g):
     non-temporal: nothing in the kernel reads the output again."""
     g.nops(20)
     T = EPI_T
+    # temporaries from register EB on: S set B past the EPI registers (dead in
+    # every last tile; S set A may hold the next pass's scores), or S set A for
+    # joint attention (one pass, and its addressing needs more registers)
+    EB = 0 if JOINT else 76
+    negm_of = negm_of or negm
     pitch = HD * 2 + 8
     lpr = HD // 8                  # lanes per output row (16 bytes each)
     rpr = 64 // lpr                # rows per store instruction
-    addr, wa, ra, t0, left, ohi = S_SET[0], 2, 3, 49, 48, 50
-    data = 16                      # v16.. read-back rows (4 per read)
+    addr, wa, ra, t0, left, ohi = EB, EB + 2, EB + 3, EB + 49, EB + 48, EB + 50
+    data = EB + 16                 # read-back rows (4 per read)
     lane = opnd(g, "lane", EPI_L + 5)
     # LDS write address: row lane % 32, + 8 bytes for the upper half-wave;
     # read address: row lane / lpr, 16-byte column lane % lpr
@@ -860,7 +866,7 @@ def epilogue(g):
     for qb in range(2):
         lt, inv, t = EPI_L + 0, EPI_L + 1, EPI_L + 2
         xa = opnd(g, "xaddr", EPI_L + 3)
-        qrow = vr(51)  # this lane's query row in this pass
+        qrow = vr(EB + 51)  # this lane's query row in this pass
         g(f"v_add_u32 {qrow}, {s_(S_QOFF)}, {opnd(g, f'qrow{qb}', EPI_L + 4)}")
         g(f"ds_bpermute_b32 {vr(t)}, {xa}, {vr(LRUN + qb)}")
         g("s_waitcnt lgkmcnt(0)")
@@ -884,14 +890,14 @@ def epilogue(g):
         # written but never stored)
         for d in range(DT):
             for gg in range(4):
-                w0, w1 = 4, 5
+                w0, w1 = EB + 4, EB + 5
                 base = o_reg(qb, d) + gg * 4
                 for k in range(4):
-                    g(f"v_accvgpr_read_b32 {vr(8 + k)}, {ar(base + k)}")
+                    g(f"v_accvgpr_read_b32 {vr(EB + 8 + k)}, {ar(base + k)}")
                 for k in range(4):
-                    g(f"v_mul_f32 {vr(8 + k)}, {vr(8 + k)}, {vr(inv)}")
-                g(f"v_cvt_pk_bf16_f32 {vr(w0)}, {vr(8)}, {vr(9)}")
-                g(f"v_cvt_pk_bf16_f32 {vr(w1)}, {vr(10)}, {vr(11)}")
+                    g(f"v_mul_f32 {vr(EB + 8 + k)}, {vr(EB + 8 + k)}, {vr(inv)}")
+                g(f"v_cvt_pk_bf16_f32 {vr(w0)}, {vr(EB + 8)}, {vr(EB + 9)}")
+                g(f"v_cvt_pk_bf16_f32 {vr(w1)}, {vr(EB + 10)}, {vr(EB + 11)}")
                 g(f"ds_write_b64 {vr(wa)}, {vr(w0, 2)} offset:{(d * 32 + gg * 8) * 2}")
         g("s_waitcnt lgkmcnt(0)")
         for i in range(32 // rpr):
@@ -907,7 +913,7 @@ def epilogue(g):
             # output while j < len_img, else to the text output; jbase[01] hold
             # the two sources' segment bases (shifted by len_img for text) plus
             # this lane's 16-byte column
-            j0, ib, tb = 52, 53, 55
+            j0, ib, tb = EB + 52, EB + 53, EB + 55
             g(f"v_subrev_u32 {vr(j0)}, %[qseg], {vr(left)}")
             g(f"v_and_b32 {vr(t0)}, {lpr - 1}, {lane}")
             g(f"v_lshlrev_b32 {vr(t0)}, 4, {vr(t0)}")
@@ -935,10 +941,10 @@ def epilogue(g):
                     g(f"v_add_u32 {vr(j0)}, {rpr}, {vr(j0)}")
                 g(f"v_mad_u64_u32 {vr(addr, 2)}, {sp(S_CMP)}, {vr(j0)}, %[ldob], 0")
                 g(f"v_cmp_gt_i32 vcc, %[lena], {vr(j0)}")
-                g(f"v_cndmask_b32 {vr(57)}, {vr(tb)}, {vr(ib)}, vcc")
-                g(f"v_cndmask_b32 {vr(58)}, {vr(tb + 1)}, {vr(ib + 1)}, vcc")
-                g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(57)}, {vr(addr)}")
-                g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(58)}, {vr(addr + 1)}, vcc")
+                g(f"v_cndmask_b32 {vr(EB + 57)}, {vr(tb)}, {vr(ib)}, vcc")
+                g(f"v_cndmask_b32 {vr(EB + 58)}, {vr(tb + 1)}, {vr(ib + 1)}, vcc")
+                g(f"v_add_co_u32 {vr(addr)}, vcc, {vr(EB + 57)}, {vr(addr)}")
+                g(f"v_addc_co_u32 {vr(addr + 1)}, vcc, {vr(EB + 58)}, {vr(addr + 1)}, vcc")
             elif i:
                 g(f"s_mov_b64 exec, {sp(S_EXEC)}")
                 g(f"v_add_co_u32 {vr(addr)}, vcc, {s_(S_T1)}, {vr(addr)}")
@@ -956,15 +962,15 @@ def epilogue(g):
         g(f"v_cmp_gt_u32 vcc, 32, {lane}")
         g("s_and_b64 exec, exec, vcc")
         g(f"s_cbranch_execz {skip}")
-        g(f"v_log_f32 {vr(12)}, {vr(lt)}")
+        g(f"v_log_f32 {vr(EB + 12)}, {vr(lt)}")
         g("s_nop 0")
-        g(f"v_sub_f32 {vr(12)}, {vr(12)}, {vr(negm(qb))}")
-        g(f"v_mul_f32 {vr(12)}, 0x3f317218, {vr(12)}")
+        g(f"v_sub_f32 {vr(EB + 12)}, {vr(EB + 12)}, {vr(negm_of(qb))}")
+        g(f"v_mul_f32 {vr(EB + 12)}, 0x3f317218, {vr(EB + 12)}")
         g(f"v_cmp_lt_f32 vcc, 0, {vr(lt)}")
-        g(f"v_mov_b32 {vr(14)}, 0xff800000")
-        g(f"v_cndmask_b32 {vr(12)}, {vr(14)}, {vr(12)}, vcc")
-        g(f"v_lshlrev_b32 {vr(13)}, 2, {qrow}")
-        g(f"global_store_dword {vr(13)}, {vr(12)}, %[lsebase]")
+        g(f"v_mov_b32 {vr(EB + 14)}, 0xff800000")
+        g(f"v_cndmask_b32 {vr(EB + 12)}, {vr(EB + 14)}, {vr(EB + 12)}, vcc")
+        g(f"v_lshlrev_b32 {vr(EB + 13)}, 2, {qrow}")
+        g(f"global_store_dword {vr(EB + 13)}, {vr(EB + 12)}, %[lsebase]")
         g.label(skip)
         g(f"s_mov_b64 exec, {sp(S_EXEC)}")
 

@@ -667,6 +667,32 @@ def last_tile(g, a):
     if multi:
         last_tile_prefetch(g, a, nopf)
     g.label(nopf)
+    # a full last tile after a steady one: P keys 0..31 and their row sums were
+    # made by that tile's phase 2, so only keys 32..63 are computed here and the
+    # check is the steady tile's; otherwise P of all 64 keys is recomputed
+    recompute = g.new_label("lastrecompute")
+    common = g.new_label("lastpv")
+    reuse_back = g.new_label("lastreuseback")
+    g(f"s_cmp_eq_u32 {s_(S_VALID)}, {BN}")
+    g(f"s_cbranch_scc0 {recompute}")
+    g(f"s_cmp_eq_u32 {s_(S_NKT1)}, 0")
+    g(f"s_cbranch_scc1 {recompute}")
+    for it in make_items(g, pair_list(1), a, a, RS1):
+        it()
+    for qb in range(2):
+        g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
+    g(f"v_cmp_nge_f32 vcc, {s_(S_THR)}, {vr(DTMP)}")
+    g(f"v_cmp_nge_f32_e64 {sp(S_CMP)}, {s_(S_THR)}, {vr(DTMP + 1)}")
+    g(f"s_or_b64 vcc, vcc, {sp(S_CMP)}")
+    g(f"s_cbranch_vccz {reuse_back}")
+    exact_rescale(g, a, a, (0, 1))
+    for qb in range(2):
+        g(f"v_add_f32 {vr(DTMP + qb)}, {vr(RS0 + qb)}, {vr(RS1 + qb)}")
+    g.label(reuse_back)
+    for qb in range(2):
+        g(f"v_add_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(DTMP + qb)}")
+    g(f"s_branch {common}")
+    g.label(recompute)
     for qb in range(2):
         g(f"v_mov_b32 {vr(RS0 + qb)}, 0")
     g(f"s_cmp_eq_u32 {s_(S_VALID)}, {BN}")
@@ -692,6 +718,7 @@ def last_tile(g, a):
     g.label(checked)
     for qb in range(2):
         g(f"v_add_f32 {vr(LRUN + qb)}, {vr(LRUN + qb)}, {vr(RS0 + qb)}")
+    g.label(common)
     g("s_nop 2")
     for f in range(4):
         v_read(g, f, a)

@@ -417,17 +417,41 @@ struct L4 {
       [b25] "v"(bv[25]), [b26] "v"(bv[26]), [b27] "v"(bv[27]), [b28] "v"(bv[28]), [b29] "v"(bv[29]),            \
       [b30] "v"(bv[30]), [b31] "v"(bv[31])
 template <int EPI, int FI>
+__device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __restrict__ A, int64_t lda,
+                                        const bf16_t* __restrict__ W, int64_t ldw, const float* __restrict__ bias,
+                                        void* __restrict__ Cv, int64_t ldc, int M, int N, int K, const bf16_t* R,
+                                        int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
+                                        const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n,
+                                        int group_m);
+template <int EPI, int FI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
     const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
+  __shared__ u32x4_t lds[L4<FI>::LDS_BYTES / 16];
+  // Persistent: XCD x (= blockIdx % 8) owns the tiles [x * per_xcd, (x + 1) *
+  // per_xcd), which its workgroups take in turn (the order a one-tile-per-
+  // workgroup launch would run them in), so each workgroup loads its kernel
+  // arguments once and a tile's k loop starts while the previous tile's
+  // stores drain.
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int ntiles = tiles_m * tiles_n, per_xcd = (ntiles + 7) / 8;
+  const int tlo = (b & 7) * per_xcd, thi = min(tlo + per_xcd, ntiles);
+  for (int L = tlo + (b >> 3); L < thi; L += nb >> 3)
+    l4_tile<EPI, FI>(lds, L, A, lda, W, ldw, bias, Cv, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, tiles_m,
+                     tiles_n, group_m);
+}
+
+template <int EPI, int FI>
+__device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __restrict__ A, int64_t lda,
+                                        const bf16_t* __restrict__ W, int64_t ldw, const float* __restrict__ bias,
+                                        void* __restrict__ Cv, int64_t ldc, int M, int N, int K, const bf16_t* R,
+                                        int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
+                                        const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n,
+                                        int group_m) {
   using G = L4<FI>;
   constexpr int GBM = G::GBM, GBN = G::GBN, WTM = G::WTM, WTN = G::WTN, STG_ROW = G::STG_ROW;
-  __shared__ u32x4_t lds[G::LDS_BYTES / 16];
-  const int nb = gridDim.x, b = blockIdx.x;
-  const int L = (b & 7) * (nb >> 3) + (b >> 3);
-  if (L >= tiles_m * tiles_n) return;
   const int group = L / (group_m * tiles_n);
   const int first_m = group * group_m;
   const int gm = min(group_m, tiles_m - first_m);
@@ -435,7 +459,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
   const int mt = first_m + pid % gm, nt = pid / gm;
   const int m0 = mt * GBM, n0 = nt * GBN;
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  // the lane's values are recomputed per tile (an opaque copy of the thread id
+  // keeps them out of the registers that stay live across the k loop)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   const int ql = lane & 15, g = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int a_row0 = (wave_u & 1) * WTM, w_row0 = (wave_u >> 1) * WTN;
@@ -484,57 +512,64 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
 #include "gemm_l4w96_body.inc"
         : : DITK_L4_OPERANDS : DITK_GEMM_L4_CLOBBERS "scc", "memory");
 
-  // epilogue on this wave's staged rows (the wave wrote them and waited for them)
+  // epilogue on this wave's staged rows (the wave wrote them and waited for them).
+  // The output (and residual) rows go through buffer descriptors whose range
+  // ends at the last row of the matrix: a store past it is dropped and a load
+  // returns 0, so the passes have no branches and the staged-row reads and
+  // residual loads of many passes are in flight together.
   constexpr int CPR = WTN / 8;                    // 16-byte units per row (16 or 12)
   constexpr int RPP = 64 / CPR;                   // rows per pass (4 or 5; lanes past RPP * CPR idle)
   constexpr int NPASS = (WTM + RPP - 1) / RPP;
   constexpr bool HAS_RES = EPI == EPI_GATE_RES || EPI == EPI_RES;
+  constexpr uint32_t kOut = 0x80000000u;          // an offset past every descriptor's range
+  const int row0 = m0 + a_row0;                   // this wave tile's first row
+  const int rows = max(0, min(WTM, M - row0));    // its rows inside the matrix
+  const uint32_t ldc2 = (uint32_t)(ldc * 2), ldr2 = (uint32_t)(ldr * 2);
+  // descriptors from wave-uniform (scalar) base addresses
+  auto sptr = [&](const void* p) {
+    const uint64_t x = (uint64_t)(uintptr_t)p;
+    const uint64_t lo = su((uint32_t)x), hi = su((uint32_t)(x >> 32));
+    return reinterpret_cast<void*>((uintptr_t)(lo | (hi << 32)));
+  };
+  const int rec_c = (int)su((uint32_t)rows * ldc2), rec_r = (int)su((uint32_t)rows * ldr2);
+  const __amdgpu_buffer_rsrc_t cdesc = __builtin_amdgcn_make_buffer_rsrc(
+      sptr(reinterpret_cast<bf16_t*>(Cv) + (int64_t)row0 * ldc + n0 + w_row0), 0, rec_c, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rdesc = __builtin_amdgcn_make_buffer_rsrc(
+      sptr(HAS_RES ? R + (int64_t)row0 * ldr + n0 + w_row0 : nullptr), 0, HAS_RES ? rec_r : 0, 0x00020000);
   const int c8 = lane % CPR;
   const int n = n0 + w_row0 + c8 * 8;
-  const int mrow = m0 + a_row0 + lane / CPR;
-  if (n >= N || lane >= RPP * CPR) return;
+  const bool lane_on = n < N && lane < RPP * CPR;   // lanes past N or past a pass's units store nothing
   const char* stage = reinterpret_cast<const char*>(lds) + wave_u * (WTM * STG_ROW);
   int seg_lo = 0;
   bool one_seg = true;
   f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
   if (EPI == EPI_GATE_RES) {
-    seg_lo = find_segment(cu, nseg, m0 + a_row0);
-    one_seg = seg_lo == find_segment(cu, nseg, min(m0 + a_row0 + WTM, M) - 1);
+    seg_lo = find_segment(cu, nseg, min(row0, M - 1));
+    one_seg = seg_lo == find_segment(cu, nseg, min(row0 + WTM, M) - 1);
     if (one_seg) {
-      const float* gp = gate + (int64_t)seg_lo * gate_stride + n;
+      const float* gp = gate + (int64_t)seg_lo * gate_stride + min(n, N - 8);
       g0 = *reinterpret_cast<const f32x4_t*>(gp);
       g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
     }
   }
-  constexpr int RB = HAS_RES ? NPASS : 1;  // every residual row loaded before the passes
-  // row pointers advanced by RPP rows per pass (no per-pass 64-bit multiplies)
-  const bf16_t* rrow = HAS_RES ? R + (int64_t)mrow * ldr + n : nullptr;
-  bf16_t* crow = reinterpret_cast<bf16_t*>(Cv) + (int64_t)mrow * ldc + n;
-  const int64_t rstep = (int64_t)RPP * ldr, cstep = (int64_t)RPP * ldc;
+  constexpr int RB = 8;  // passes per batch: staged reads and residual loads issued together
 #pragma unroll
   for (int r0 = 0; r0 < NPASS; r0 += RB) {
-    u32x4_t res[RB];
-    if (HAS_RES) {
+    u32x4_t v[RB], res[RB];
+    uint32_t off[RB];
 #pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        const int m = mrow + (r0 + q) * RPP;
-        const bool in = m < M && (r0 + q) * RPP + lane / CPR < WTM;
-        res[q] = in ? *reinterpret_cast<const u32x4_t*>(rrow) : u32x4_t{0, 0, 0, 0};
-        rrow += rstep;
-      }
+    for (int q = 0; q < RB && r0 + q < NPASS; ++q) {
+      const int t = (r0 + q) * RPP + lane / CPR;  // row in the wave tile
+      off[q] = t < rows && lane_on ? (uint32_t)t * ldc2 + c8 * 16 : kOut;
+      v[q] = *reinterpret_cast<const u32x4_t*>(stage + min(t, WTM - 1) * STG_ROW + c8 * 16);
+      if (HAS_RES)
+        res[q] = __builtin_amdgcn_raw_buffer_load_b128(rdesc, t < rows && lane_on ? (uint32_t)t * ldr2 + c8 * 16 : kOut, 0, 0);
     }
 #pragma unroll
-    for (int q = 0; q < RB; ++q) {
-      const int r = r0 + q;
-      const int t = r * RPP + lane / CPR;
-      const int m = mrow + r * RPP;
-      bf16_t* cp = crow;
-      crow += cstep;
-      if (m >= M || t >= WTM) continue;
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + t * STG_ROW + c8 * 16);
+    for (int q = 0; q < RB && r0 + q < NPASS; ++q) {
       if (EPI != EPI_BIAS) {
         float x[8];
-        unpack8(v, x);
+        unpack8(v[q], x);
         if (EPI == EPI_GELU) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = gelu_tanh_f(x[e]);
@@ -543,11 +578,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
           for (int e = 0; e < 8; ++e) x[e] = silu_f(x[e]);
         } else {
           float rv[8];
-          unpack8(res[HAS_RES ? q : 0], rv);
+          unpack8(res[q], rv);
           if (EPI == EPI_GATE_RES) {
             f32x4_t h0 = g0, h1 = g1;
             if (!one_seg) {
-              const float* gp = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+              const int m = min(row0 + (r0 + q) * RPP + lane / CPR, M - 1);
+              const float* gp = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + min(n, N - 8);
               h0 = *reinterpret_cast<const f32x4_t*>(gp);
               h1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
             }
@@ -561,21 +597,31 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
             for (int e = 0; e < 8; ++e) x[e] = rv[e] + x[e];
           }
         }
-        v = pack8(x);
+        v[q] = pack8(x);
       }
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(cp));
+      __builtin_amdgcn_raw_buffer_store_b128(v[q], cdesc, off[q], 0, 2);  // non-temporal
     }
   }
 }
 
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
 template <int EPI, int FI>
 int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
               int M, int N, int K, const void* R, int64_t ldr, const float* gate, int64_t gate_stride,
               const int32_t* cu, int nseg, hipStream_t stream) {
   constexpr int GBN = L4<FI>::GBN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + GBN - 1) / GBN;
-  const int64_t nblocks = ((int64_t)tiles_m * tiles_n + 7) / 8 * 8;
-  DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
+  // one persistent workgroup per CU (a multiple of 8: the same number per XCD)
+  const int64_t nblocks = std::min<int64_t>(((int64_t)tiles_m * tiles_n + 7) / 8 * 8, cu_count() / 8 * 8);
   gemm_kernel_l4<EPI, FI><<<(unsigned)nblocks, 256, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
       gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
@@ -595,16 +641,6 @@ bool use_l4(int N, int K) { return K % 64 == 0 && (N >= 3072 || K >= 4096); }
 // one round with a quarter of the CUs idle; N = 4608 is 768 tiles = 3 rounds
 // instead of 576 = 2.25 (so 3).  Ties keep the 256-wide tiles (fewer bytes
 // moved per FLOP).
-int cu_count() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-  }
-  return cached[dev];
-}
 bool use_w192(int M, int N) {
   const int64_t tm = (M + 255) / 256, ncu = cu_count();
   const int64_t r256 = (tm * ((N + 255) / 256) + ncu - 1) / ncu, r192 = (tm * ((N + 191) / 192) + ncu - 1) / ncu;
@@ -641,9 +677,11 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   const int64_t large_tiles = (int64_t)((M + L::GBM - 1) / L::GBM) * ((N + L::GBN - 1) / L::GBN);
   if (large_tiles < kSmallBelow)
     return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
-  if (EPI != EPI_F32 && K % 64 == 0 && use_w192(M, N))
+  // the large-tile kernel's epilogue addresses a wave tile's rows by 32-bit offsets
+  const bool l4_strides = ldc < (1 << 22) && ldr < (1 << 22);
+  if (EPI != EPI_F32 && K % 64 == 0 && l4_strides && use_w192(M, N))
     return launch_l4<EPI, 6>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
-  if (EPI != EPI_F32 && use_l4(N, K))
+  if (EPI != EPI_F32 && l4_strides && use_l4(N, K))
     return launch_l4<EPI, 8>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }

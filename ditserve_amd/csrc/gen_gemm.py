@@ -178,6 +178,10 @@ def stage(g, buf, first=False, last_check=None):
 
 
 def prologue(g):
+    # a persistent workgroup's previous tile: every wave's reads of its staged
+    # rows are done before the stage DMAs overwrite them
+    g("s_waitcnt lgkmcnt(0)")
+    g("s_barrier")
     g(f"s_add_u32 s{S_SW}, %[lds], %[wave1k]")
     g(f"s_sub_u32 s{S_NK1}, %[nk], 1")
     g(f"s_mov_b32 s{S_S}, 0")

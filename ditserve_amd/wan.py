@@ -391,26 +391,39 @@ class WanTransformer:
         return self.prediction_packed(packet)
 
 
+_SLOT_ROPE = {}
+
+
 def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
     """Drop-in for the reference's `fused_qk_norm_rope` slot
     (transformer_wan.py:24-25,111-115): query/key [B, S, D] bf16, norm_q/norm_k
     modules or tensors holding the RMSNorm weight, freqs_cos/sin [1, S, 1, Dh]
     fp32 tables (repeat-interleaved, as WanRotaryPosEmbed returns them).
-    Returns q, k as [B, S, H, Dh] bf16 (new tensors; inputs untouched)."""
+    Returns q, k as [B, S, H, Dh] bf16 (new tensors; inputs untouched).
+
+    One kernel launch covers the B requests (each a segment of S tokens whose
+    position is its index on a single axis); the rotation tables and segment
+    table built from freqs_cos/sin are kept for the next call with the same
+    tables, so a steady call allocates only the two outputs."""
     B, S, D = query.shape
     dh = D // heads
     wq = getattr(norm_q, "weight", norm_q).float().contiguous()
     wk = getattr(norm_k, "weight", norm_k).float().contiguous()
-    # per-token tables: pair i uses cos[..., 2i] / sin[..., 2i+1]; treat every
-    # token as its own position on a single "axis" (max_pos = S).
-    cos_tab = freqs_cos.reshape(S, dh)[:, 0::2].float().contiguous()
-    sin_tab = freqs_sin.reshape(S, dh)[:, 1::2].float().contiguous()
-    seg = Segments([0, S], query.device)
-    rope = ops.Rope(cos_tab, sin_tab, [(S, 1, 1)], seg, dh // 2, 0)
-    q = query.reshape(B * S, D).to(_BF16).clone()
-    k = key.reshape(B * S, D).to(_BF16).clone()
-    for b in range(B):
-        ops.qk_norm_rope_(q[b * S:(b + 1) * S], k[b * S:(b + 1) * S], wq, wk, dh, 1e-6, rope=rope)
+    key_ = (query.device, B, S, dh, freqs_cos.data_ptr(), freqs_cos._version, freqs_sin.data_ptr(),
+            freqs_sin._version)
+    rope = _SLOT_ROPE.get(key_)
+    if rope is None:
+        # per-token tables: pair i uses cos[..., 2i] / sin[..., 2i+1]
+        cos_tab = freqs_cos.reshape(S, dh)[:, 0::2].float().contiguous()
+        sin_tab = freqs_sin.reshape(S, dh)[:, 1::2].float().contiguous()
+        seg = Segments([b * S for b in range(B + 1)], query.device)
+        rope = ops.Rope(cos_tab, sin_tab, [(S, 1, 1)] * B, seg, dh // 2, 0)
+        if len(_SLOT_ROPE) >= 8:
+            _SLOT_ROPE.clear()
+        _SLOT_ROPE[key_] = rope
+    q = query.reshape(B * S, D).to(_BF16, copy=True)
+    k = key.reshape(B * S, D).to(_BF16, copy=True)
+    ops.qk_norm_rope_(q, k, wq, wk, dh, 1e-6, rope=rope)
     return q.reshape(B, S, heads, dh), k.reshape(B, S, heads, dh)
 
 

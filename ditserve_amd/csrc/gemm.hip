@@ -630,10 +630,13 @@ int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
 
 // The one-wave-per-SIMD kernel where it measured faster than gemm_kernel's large
 // tiles (same box, Wan2.1 block shapes at M = 65520): N >= 3072 or K >= 4096
-// (qkv -3.4%, ffn-up -2.9%, ffn-down -4.7%, N = 3072 SiLU -3.3%).  At N = K = 1536
-// its per-tile prologue and epilogue weigh more and it was 6-8% slower.  The
-// choice changes no result.
-bool use_l4(int N, int K) { return K % 64 == 0 && (N >= 3072 || K >= 4096); }
+// (qkv -3.4%, ffn-up -2.9%, ffn-down -4.7%, N = 3072 SiLU -3.3%), and, since its
+// workgroups are persistent, at N = K = 1536 too except with the gated residual
+// (bias -4%, residual -4%; gated residual +3%, also with the gate looked up
+// before the k loop).  The choice changes no result.
+bool use_l4(int N, int K, int epi) {
+  return K % 64 == 0 && (N >= 3072 || K >= 4096 || epi != EPI_GATE_RES);
+}
 
 // 256 x 192 tiles when they fill the GPU's CUs in fewer tile-rounds, weighted
 // by tile width, than 256 x 256 ones (the two take the same time per unit of
@@ -681,7 +684,7 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
   const bool l4_strides = ldc < (1 << 22) && ldr < (1 << 22);
   if (EPI != EPI_F32 && K % 64 == 0 && l4_strides && use_w192(M, N))
     return launch_l4<EPI, 6>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
-  if (EPI != EPI_F32 && l4_strides && use_l4(N, K))
+  if (EPI != EPI_F32 && l4_strides && use_l4(N, K, EPI))
     return launch_l4<EPI, 8>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
 }

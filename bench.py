@@ -42,7 +42,7 @@ SCHEDULE_STEPS = 50
 # over this bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that
 # counter's reading for the CALIB_BYTES copy: FETCH 884792 KiB x 1.9998, WRITE
 # 196560 KiB x 1.0000 (profiles/wan21_480p_cfg2_step_traffic.md).
-ATTN_SELF_TRAFFIC_BYTES = (884792 * 1.9998 + 196560 * 1.0000) * 1024
+ATTN_SELF_TRAFFIC_BYTES = (884805 * 1.9998 + 196560 * 1.0000) * 1024
 
 WAN21_METRIC = "denoise steps/s & tokens/s, Wan2.1-1.3B 480p-81f CFG2; attn % bf16 MFMA peak"
 WORKLOADS = {

@@ -40,7 +40,7 @@ GUIDANCE = 5.0
 SCHEDULE_STEPS = 50
 # HBM traffic of one headline self-attention launch, from two rocprofv3 --pmc passes
 # over this bench (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by that
-# counter's reading for the CALIB_BYTES copy: FETCH 884792 KiB x 1.9998, WRITE
+# counter's reading for the CALIB_BYTES copy: FETCH 884805 KiB x 1.9998, WRITE
 # 196560 KiB x 1.0000 (profiles/wan21_480p_cfg2_step_traffic.md).
 ATTN_SELF_TRAFFIC_BYTES = (884805 * 1.9998 + 196560 * 1.0000) * 1024
 

@@ -107,6 +107,35 @@ def test_gemm_tile_configs_agree(epi, K, N):
     assert torch.equal(full[lo:hi], part)
 
 
+@pytest.mark.parametrize("epi", ["bias", "res", "gate_res", "gelu"])
+def test_gemm_persistent_tiles_agree(epi):
+    """M = 20000, N = K = 1536: 474 large tiles on at most 256 persistent
+    workgroups (some take two), the last tile row ragged (20000 = 78 x 256 + 32).
+    Rows computed there equal, bitwise, the same rows computed alone by the
+    small-tile kernel: a slice ending at the last row and one across tile rows."""
+    ops = _ops()
+    M, N, K = 20000, 1536, 1536
+    a = randn((M, K), 50).to(DEV, torch.bfloat16)
+    w = randn((N, K), 51, 0.02).to(DEV, torch.bfloat16)
+    b = randn((N,), 52).to(DEV)
+    r = randn((M, N), 53).to(DEV, torch.bfloat16)
+    gate = randn((2, N), 54).to(DEV)
+    cut = 12345
+
+    def run(lo, hi):
+        kw = {}
+        if epi == "gate_res":
+            kw = dict(residual=r[lo:hi].contiguous(), gate=gate,
+                      segments=_seg([0, min(max(cut - lo, 0), hi - lo), hi - lo]))
+        elif epi == "res":
+            kw = dict(residual=r[lo:hi].contiguous())
+        return ops.linear(a[lo:hi].contiguous(), w, b, epi, **kw)
+
+    full = run(0, M)
+    for lo, hi in ((M - 633, M), (cut - 300, cut + 333)):
+        assert torch.equal(full[lo:hi], run(lo, hi)), (epi, lo, hi)
+
+
 def test_gemm_stage_depths_agree():
     """K % 64 == 0 runs 64-k LDS stages, otherwise 32-k stages; the MFMA k order is
     the same, so zero-padding K by 32 (forcing the 32-k path) changes no bit."""

@@ -621,7 +621,7 @@ int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
   constexpr int GBN = L4<FI>::GBN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + GBN - 1) / GBN;
   // one persistent workgroup per CU (a multiple of 8: the same number per XCD)
-  const int64_t nblocks = std::min<int64_t>(((int64_t)tiles_m * tiles_n + 7) / 8 * 8, cu_count() / 8 * 8);
+  const int64_t nblocks = std::min<int64_t>(((int64_t)tiles_m * tiles_n + 7) / 8 * 8, std::max(8, cu_count() / 8 * 8));
   gemm_kernel_l4<EPI, FI><<<(unsigned)nblocks, 256, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
       gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));

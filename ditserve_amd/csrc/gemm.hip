@@ -552,18 +552,26 @@ __device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __res
       g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
     }
   }
-  constexpr int RB = 8;  // passes per batch: staged reads and residual loads issued together
+  // every residual row is loaded first (one latency for the tile), then the
+  // staged rows are read and stored in batches of RB passes
+  u32x4_t res[HAS_RES ? NPASS : 1];
+  if (HAS_RES) {
+#pragma unroll
+    for (int r = 0; r < NPASS; ++r) {
+      const int t = r * RPP + lane / CPR;
+      res[r] = __builtin_amdgcn_raw_buffer_load_b128(rdesc, t < rows && lane_on ? (uint32_t)t * ldr2 + c8 * 16 : kOut, 0, 0);
+    }
+  }
+  constexpr int RB = 8;
 #pragma unroll
   for (int r0 = 0; r0 < NPASS; r0 += RB) {
-    u32x4_t v[RB], res[RB];
+    u32x4_t v[RB];
     uint32_t off[RB];
 #pragma unroll
     for (int q = 0; q < RB && r0 + q < NPASS; ++q) {
       const int t = (r0 + q) * RPP + lane / CPR;  // row in the wave tile
       off[q] = t < rows && lane_on ? (uint32_t)t * ldc2 + c8 * 16 : kOut;
       v[q] = *reinterpret_cast<const u32x4_t*>(stage + min(t, WTM - 1) * STG_ROW + c8 * 16);
-      if (HAS_RES)
-        res[q] = __builtin_amdgcn_raw_buffer_load_b128(rdesc, t < rows && lane_on ? (uint32_t)t * ldr2 + c8 * 16 : kOut, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < RB && r0 + q < NPASS; ++q) {
@@ -578,7 +586,7 @@ __device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __res
           for (int e = 0; e < 8; ++e) x[e] = silu_f(x[e]);
         } else {
           float rv[8];
-          unpack8(res[q], rv);
+          unpack8(res[HAS_RES ? r0 + q : 0], rv);
           if (EPI == EPI_GATE_RES) {
             f32x4_t h0 = g0, h1 = g1;
             if (!one_seg) {

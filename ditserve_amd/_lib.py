@@ -24,6 +24,8 @@ SIGNATURES = {
     "ditk_modulation": (c_int, [_P, _P, _P, c_int, c_int, _P]),
     "ditk_qk_norm_rope": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, _P, _P, c_float, c_int, _P,
                                   _P, c_int, _P, _P, c_int, c_int, c_int, _P]),
+    "ditk_qk_norm_rope_out": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, _P,
+                                      _P, c_float, c_int, _P, _P, c_int, _P, _P, c_int, c_int, c_int, _P]),
     "ditk_gemm": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int, c_int, c_int, c_int, _P, c_int64,
                           _P, c_int64, _P, c_int, _P]),
     "ditk_vt_columns": (c_int64, [c_int64, c_int]),

@@ -210,7 +210,8 @@ __device__ __forceinline__ void norm_rotate_store(bf16_t* __restrict__ xr, const
 
 template <int GROUP_LANES, int NC>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
-    bf16_t* __restrict__ q, int64_t ldq, bf16_t* __restrict__ k, int64_t ldk, int T, int D,
+    const bf16_t* q, int64_t ldq, const bf16_t* k, int64_t ldk, bf16_t* qo, int64_t ldqo, bf16_t* ko,
+    int64_t ldko, int T, int D,
     int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
     const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
@@ -221,8 +222,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= T) return;
-  bf16_t* qr = q + (int64_t)row * ldq;
-  bf16_t* kr = k + (int64_t)row * ldk;
+  // q/k may be the outputs themselves (in place): a lane reads its row chunks
+  // before it writes them, and no other lane touches them
+  const bf16_t* qr = q + (int64_t)row * ldq;
+  const bf16_t* kr = k + (int64_t)row * ldk;
   const int nchunk = D >> 3;
   u32x4_t rawq[NC], rawk[NC];
 #pragma unroll
@@ -274,8 +277,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     load_w<NC>(wq, nchunk, lane, wq4);
     load_w<NC>(wk, nchunk, lane, wk4);
   }
-  norm_rotate_store<NC>(qr, rawq, rsq, wq4, rope, rc, rsn, nchunk, lane);
-  norm_rotate_store<NC>(kr, rawk, rsk, wk4, rope, rc, rsn, nchunk, lane);
+  norm_rotate_store<NC>(qo + (int64_t)row * ldqo, rawq, rsq, wq4, rope, rc, rsn, nchunk, lane);
+  norm_rotate_store<NC>(ko + (int64_t)row * ldko, rawk, rsk, wk4, rope, rc, rsn, nchunk, lane);
 }
 
 }  // namespace
@@ -332,16 +335,19 @@ DITK_EXPORT int ditk_modulation(const float* table, const float* proj, float* mo
   return ditk_check_launch("ditk_modulation");
 }
 
-DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D,
-                                  int head_dim, const float* wq, const float* wk, float eps,
-                                  int per_head, const float* rope_cos, const float* rope_sin,
-                                  int max_pos, const int32_t* cu_seqlens, const int32_t* grids,
-                                  int nseg, int t_pairs, int h_pairs, hipStream_t stream) {
-  DITK_REQUIRE(q && k && wq && wk, "ditk_qk_norm_rope: null tensor");
+namespace {
+int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, void* qo, int64_t ldqo, void* ko,
+                        int64_t ldko, int T, int D, int head_dim, const float* wq, const float* wk, float eps,
+                        int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
+                        const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
+                        hipStream_t stream) {
+  DITK_REQUIRE(q && k && qo && ko && wq && wk, "ditk_qk_norm_rope: null tensor");
   DITK_REQUIRE(D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks, "ditk_qk_norm_rope: bad D=%d", D);
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_qk_norm_rope: head_dim must be 64 or 128");
   DITK_REQUIRE(D % head_dim == 0, "ditk_qk_norm_rope: D %% head_dim != 0");
-  DITK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0, "ditk_qk_norm_rope: leading dims must be multiples of 8");
+  DITK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldqo % 8 == 0 && ldko % 8 == 0,
+               "ditk_qk_norm_rope: leading dims must be multiples of 8");
+  DITK_REQUIRE(((uintptr_t)qo % 16) == 0 && ((uintptr_t)ko % 16) == 0, "ditk_qk_norm_rope: outputs must be 16-byte aligned");
   DITK_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)wq % 16) == 0 &&
                ((uintptr_t)wk % 16) == 0, "ditk_qk_norm_rope: tensors must be 16-byte aligned");
   DITK_REQUIRE(rope_cos == nullptr || (rope_sin && cu_seqlens && grids && nseg > 0 && max_pos > 0),
@@ -356,7 +362,8 @@ DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, in
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
 #define DITK_QKN(G, NCV)                                                                                  \
-  qk_norm_rope_kernel<G, NCV><<<grid, 256, 0, stream>>>((bf16_t*)q, ldq, (bf16_t*)k, ldk, T, D, head_dim, \
+  qk_norm_rope_kernel<G, NCV><<<grid, 256, 0, stream>>>((const bf16_t*)q, ldq, (const bf16_t*)k, ldk,    \
+                                                        (bf16_t*)qo, ldqo, (bf16_t*)ko, ldko, T, D, head_dim, \
                                                         wq, wk, eps, rope_cos, rope_sin, max_pos,         \
                                                         cu_seqlens, grids, nseg, t_pairs, h_pairs)
 #define DITK_QKN_NC(G)              \
@@ -380,4 +387,24 @@ DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, in
 #undef DITK_QKN_NC
 #undef DITK_QKN
   return ditk_check_launch("ditk_qk_norm_rope");
+}
+}  // namespace
+
+DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D,
+                                  int head_dim, const float* wq, const float* wk, float eps,
+                                  int per_head, const float* rope_cos, const float* rope_sin,
+                                  int max_pos, const int32_t* cu_seqlens, const int32_t* grids,
+                                  int nseg, int t_pairs, int h_pairs, hipStream_t stream) {
+  return qk_norm_rope_launch(q, ldq, k, ldk, q, ldq, k, ldk, T, D, head_dim, wq, wk, eps, per_head, rope_cos,
+                             rope_sin, max_pos, cu_seqlens, grids, nseg, t_pairs, h_pairs, stream);
+}
+
+DITK_EXPORT int ditk_qk_norm_rope_out(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out,
+                                      int64_t ldqo, void* k_out, int64_t ldko, int T, int D, int head_dim,
+                                      const float* wq, const float* wk, float eps, int per_head,
+                                      const float* rope_cos, const float* rope_sin, int max_pos,
+                                      const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs,
+                                      int h_pairs, hipStream_t stream) {
+  return qk_norm_rope_launch(q, ldq, k, ldk, q_out, ldqo, k_out, ldko, T, D, head_dim, wq, wk, eps, per_head,
+                             rope_cos, rope_sin, max_pos, cu_seqlens, grids, nseg, t_pairs, h_pairs, stream);
 }

@@ -198,10 +198,12 @@ class Rope:
             t.record_stream(stream)
 
 
-def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None):
+def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None, out=None):
     """In place: RMSNorm(q), RMSNorm(k) (across all heads, or per head) then 3D RoPE.
 
     q, k: [T, D] bf16 row views (e.g. column slices of a fused QKV buffer).
+    out: optional (q_out, k_out) [T, D] bf16 row views written instead (q, k
+    then stay untouched); returns the tensors written.
     The reference's `fused_qk_norm_rope` slot contract
     (workers/xfuser/model_executor/models/transformers/transformer_wan.py:24-25,111-115)."""
     _check(q, "q", _BF16, 2)
@@ -221,9 +223,19 @@ def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None):
             raise ValueError("rope segments do not cover q")
         args = (_ptr(rope.cos), _ptr(rope.sin), rope.cos.shape[0], _ptr(rope.segments.dev), _ptr(rope.grids),
                 rope.segments.nseg, rope.t_pairs, rope.h_pairs)
-    _lib.call("ditk_qk_norm_rope", _ptr(q), ldq, _ptr(k), ldk, T, D, head_dim, _ptr(wq), _ptr(wk), float(eps),
-              int(bool(per_head)), *args, _stream())
-    return q, k
+    if out is None:
+        _lib.call("ditk_qk_norm_rope", _ptr(q), ldq, _ptr(k), ldk, T, D, head_dim, _ptr(wq), _ptr(wk), float(eps),
+                  int(bool(per_head)), *args, _stream())
+        return q, k
+    qo, ko = out
+    for t, n in ((qo, "q_out"), (ko, "k_out")):
+        _check(t, n, _BF16, 2)
+        if t.shape != q.shape:
+            raise ValueError(f"{n} must have q's shape {tuple(q.shape)}")
+    _lib.call("ditk_qk_norm_rope_out", _ptr(q), ldq, _ptr(k), ldk, _ptr(qo), _rows(qo, "q_out"), _ptr(ko),
+              _rows(ko, "k_out"), T, D, head_dim, _ptr(wq), _ptr(wk), float(eps), int(bool(per_head)), *args,
+              _stream())
+    return qo, ko
 
 
 # ---------------------------------------------------------------------------

@@ -401,10 +401,11 @@ def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
     fp32 tables (repeat-interleaved, as WanRotaryPosEmbed returns them).
     Returns q, k as [B, S, H, Dh] bf16 (new tensors; inputs untouched).
 
-    One kernel launch covers the B requests (each a segment of S tokens whose
-    position is its index on a single axis); the rotation tables and segment
-    table built from freqs_cos/sin are kept for the next call with the same
-    tables, so a steady call allocates only the two outputs."""
+    One out-of-place kernel launch covers the B requests (each a segment of S
+    tokens whose position is its index on a single axis) and writes the new
+    tensors directly; the rotation tables and segment table built from
+    freqs_cos/sin are kept for the next call with the same tables, so a steady
+    call allocates only the two outputs."""
     B, S, D = query.shape
     dh = D // heads
     wq = getattr(norm_q, "weight", norm_q).float().contiguous()
@@ -421,9 +422,14 @@ def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
         if len(_SLOT_ROPE) >= 8:
             _SLOT_ROPE.clear()
         _SLOT_ROPE[key_] = rope
-    q = query.reshape(B * S, D).to(_BF16, copy=True)
-    k = key.reshape(B * S, D).to(_BF16, copy=True)
-    ops.qk_norm_rope_(q, k, wq, wk, dh, 1e-6, rope=rope)
+    qi, ki = query.reshape(B * S, D), key.reshape(B * S, D)
+    if qi.dtype != _BF16 or qi.stride(1) != 1:
+        qi = qi.to(_BF16).contiguous()
+    if ki.dtype != _BF16 or ki.stride(1) != 1:
+        ki = ki.to(_BF16).contiguous()
+    q = torch.empty((B * S, D), dtype=_BF16, device=query.device)
+    k = torch.empty((B * S, D), dtype=_BF16, device=query.device)
+    ops.qk_norm_rope_(qi, ki, wq, wk, dh, 1e-6, rope=rope, out=(q, k))
     return q.reshape(B, S, heads, dh), k.reshape(B, S, heads, dh)
 
 

@@ -64,6 +64,19 @@ int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D, 
                       int h_pairs, ditk_stream_t stream);
 
 /*
+ * The same, out of place: q/k rows are read and the normalized, rotated rows
+ * written to q_out/k_out (leading dims ldqo/ldko; may equal q/k).  One pass over
+ * the rows, so returning new tensors costs no separate copy.
+ * Replaces: the fused_qk_norm_rope slot, which returns new q/k tensors and
+ *   leaves its inputs untouched — transformer_wan.py:24-25,111-115.
+ */
+int ditk_qk_norm_rope_out(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out, int64_t ldqo,
+                          void* k_out, int64_t ldko, int T, int D, int head_dim, const float* wq, const float* wk,
+                          float eps, int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
+                          const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
+                          ditk_stream_t stream);
+
+/*
  * bf16 MFMA GEMM  C = epilogue(A[M,K] W[N,K]^T + bias[N]) with epilogue
  *   0 bias, 1 GELU-tanh, 2 gated residual R + bf16(y) * gate[seg] (fp32 math),
  *   3 residual R + bf16(y), 4 fp32 output, 5 SiLU.

@@ -203,6 +203,33 @@ def test_qk_norm_rope_matches_oracle():
         assert_close(kd[s0:s1].float().cpu(), rk.flatten(1), cos_min=0.99999, rel_max=5e-3, label="k")
 
 
+def test_qk_norm_rope_out_of_place_bitwise():
+    """The out-of-place entry writes exactly what the in-place one leaves, into
+    strided column slices of another buffer, and leaves its inputs untouched;
+    rope and per-head forms."""
+    ops = _ops()
+    from ditserve_amd.wan import rope_axis_pairs, rope_tables
+    D, Dh = 1536, 128
+    grids = [(2, 3, 5), (1, 4, 4)]
+    cu = [0, 30, 46]
+    T = cu[-1]
+    q = randn((T, D), 60, 2.0).to(DEV, torch.bfloat16)
+    k = randn((T, D), 61, 2.0).to(DEV, torch.bfloat16)
+    wq, wk = (randn((D,), 62, 0.1) + 1).to(DEV), (randn((D,), 63, 0.1) + 1).to(DEV)
+    cos_t, sin_t = rope_tables(Dh, 1024, 10000.0, DEV)
+    tp, hp, _ = rope_axis_pairs(Dh)
+    rope = ops.Rope(cos_t, sin_t, grids, _seg(cu), tp, hp)
+    for per_head, rp in ((False, rope), (True, None)):
+        qi, ki = q.clone(), k.clone()
+        ops.qk_norm_rope_(qi, ki, wq, wk, Dh, per_head=per_head, rope=rp)
+        buf = torch.zeros((T, 3 * D), dtype=torch.bfloat16, device=DEV)
+        qo, ko = ops.qk_norm_rope_(q, k, wq, wk, Dh, per_head=per_head, rope=rp, out=(buf[:, :D], buf[:, 2 * D:]))
+        assert torch.equal(qo, qi) and torch.equal(ko, ki)
+        assert torch.equal(buf[:, D:2 * D], torch.zeros_like(buf[:, D:2 * D]))
+    assert torch.equal(q, randn((T, D), 60, 2.0).to(DEV, torch.bfloat16))
+    assert torch.equal(k, randn((T, D), 61, 2.0).to(DEV, torch.bfloat16))
+
+
 def test_qk_norm_per_head_no_rope():
     ops = _ops()
     T, D, Dh = 100, 1536, 64

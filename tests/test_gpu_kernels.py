@@ -284,6 +284,35 @@ def test_attention_sharp_logits():
 
 
 @pytest.mark.parametrize("Dh", [128, 64])
+def test_attention_lse_merge_invariance(Dh):
+    """Attention over a key range equals the LSE-weighted merge of attention over
+    its two halves: O = (O1 e^lse1 + O2 e^lse2) / (e^lse1 + e^lse2), lse =
+    log(e^lse1 + e^lse2) -- ties the kernel's output and its natural-log LSE
+    together without restating the kernel's arithmetic.  Split at 700 (inside a
+    key tile) of 1500 keys, two segments."""
+    ops = _ops()
+    H = 2
+    cu_q, cu_k = [0, 300, 800], [0, 1500, 3000]
+    q, k, v = _attn_case(cu_q, cu_k, H, Dh, 70, scale_in=2.0)
+    qd, kd, vd = (t.to(DEV, torch.bfloat16) for t in (q, k, v))
+    o, lse = ops.flash_attn_varlen(qd, kd, vd, _seg(cu_q), _seg(cu_k), H, Dh, return_lse=True)
+    parts = []
+    for lo, hi in ((0, 700), (700, 1500)):
+        rows = torch.cat([torch.arange(b + lo, b + hi) for b in cu_k[:-1]]).to(DEV)
+        ck = [0, hi - lo, 2 * (hi - lo)]
+        parts.append(ops.flash_attn_varlen(qd, kd[rows].contiguous(), vd[rows].contiguous(), _seg(cu_q), _seg(ck), H,
+                                           Dh, return_lse=True))
+    (o1, l1), (o2, l2) = parts
+    l1, l2 = l1.float().t().contiguous(), l2.float().t().contiguous()  # [T, H]
+    m = torch.maximum(l1, l2)
+    w1, w2 = torch.exp(l1 - m), torch.exp(l2 - m)
+    o1, o2 = o1.float().view(-1, H, Dh), o2.float().view(-1, H, Dh)
+    merged = (o1 * w1[..., None] + o2 * w2[..., None]) / (w1 + w2)[..., None]
+    assert_close(o.float().view(-1, H, Dh).cpu(), merged.cpu(), cos_min=0.9999, rel_max=1e-2, label="merged O")
+    assert torch.allclose(lse.float().t().cpu(), (m + torch.log(w1 + w2)).cpu(), atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("Dh", [128, 64])
 def test_attention_rising_scores(Dh):
     """Scores rising by 0.3 per key (about 14 log2 units per 32 keys) for even query rows and
     falling for odd ones: the running max has to be raised in every half tile, inside the key

@@ -568,3 +568,11 @@ def test_invalid_arguments_raise_before_launch():
         ops.flash_attn_varlen(x, x, x, _seg([0, 10]), _seg([0, 10]), 1, 96)  # head_dim 96 unsupported
     with pytest.raises(ValueError):
         ops.linear(x, torch.zeros((8, 64), dtype=torch.bfloat16, device=DEV))  # K mismatch
+    q = torch.zeros((4, 128), dtype=torch.bfloat16, device=DEV)
+    w = torch.ones((128,), dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError):  # out-of-place output of another shape
+        ops.qk_norm_rope_(q, q.clone(), w, w, 64, out=(torch.empty((4, 64), dtype=torch.bfloat16, device=DEV), q.clone()))
+    big = torch.zeros((4, 136), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises((ValueError, DitkError)):  # output rows not 16-byte aligned (4-element column offset)
+        ops.qk_norm_rope_(q, q.clone(), w, w, 64, out=(big[:, 4:132], q.clone()))
+    assert torch.equal(q, torch.zeros_like(q))

@@ -378,16 +378,17 @@ def test_attention_q_prescaled(Dh, case, lens):
 
 @pytest.mark.parametrize("Dh", [128, 64])
 @pytest.mark.parametrize("pre", [False, True])
-def test_attention_query_tile_passes_bitwise(Dh, pre):
+@pytest.mark.parametrize("cu_k", [[0, 300, 377, 377], [0, 40, 104, 104]])
+def test_attention_query_tile_passes_bitwise(Dh, pre, cu_k):
     """Short key ranges over many query tiles run several query tiles per workgroup, the
     next tile's loads issued under the current one's last key tile.  With 16 heads the call
     takes that path; one head at a time (too few tiles to fill the GPU that way) runs one
     tile per workgroup: the outputs must be bitwise equal.  Segments: 65 query tiles (the
-    last work item one pass short) over 5 key tiles, 64 over 2, and 2 over none; sampled
-    rows are checked against the oracle."""
+    last work item one pass short) over 5 key tiles (or one partial tile), 64 over 2 (or one
+    full tile), and 2 over none; sampled rows are checked against the oracle."""
     ops = _ops()
     H = 16
-    cu_q, cu_k = [0, 16484, 32768, 33280], [0, 300, 377, 377]
+    cu_q = [0, 16484, 32768, 33280]
     g = torch.Generator(device=DEV).manual_seed(98)
     q = torch.randn((cu_q[-1], H * Dh), generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn((cu_k[-1], H * Dh), generator=g, device=DEV).to(torch.bfloat16)

@@ -646,16 +646,18 @@ bool use_l4(int N, int K, int epi) {
   return K % 64 == 0 && (N >= 3072 || K >= 4096 || epi != EPI_GATE_RES);
 }
 
-// 256 x 192 tiles when they fill the GPU's CUs in fewer tile-rounds, weighted
-// by tile width, than 256 x 256 ones (the two take the same time per unit of
-// width): e.g. M = 8192 and N = 1536 is 256 tiles = one round instead of 192 =
-// one round with a quarter of the CUs idle; N = 4608 is 768 tiles = 3 rounds
-// instead of 576 = 2.25 (so 3).  Ties keep the 256-wide tiles (fewer bytes
-// moved per FLOP).
+// 256 x 192 tiles when they fill the GPU's CUs in fewer tile-rounds than
+// 256 x 256 ones, a 192-wide tile taking 0.85 of a 256-wide one's time (measured
+// 0.82-0.88 at M = 54560, K = 3072-14336: its k loop moves the same token rows
+// for 3/4 of the MFMAs): e.g. M = 8192 and N = 1536 is 256 tiles = one round
+// instead of 192 = one round with a quarter of the CUs idle (SD3.5: ffn-down
+// -12%); N = 4608 is 768 tiles = 3 rounds instead of 576 = 2.25, so 3 (SD3.5
+// qkv -16%); but M = 54560 and N = 3072 is 3424 tiles = 14 rounds instead of
+// 2568 = 11 (Wan2.2-5B: ffn-down -11%, qkv -8%, o-proj -6% with 256-wide tiles).
 bool use_w192(int M, int N) {
   const int64_t tm = (M + 255) / 256, ncu = cu_count();
   const int64_t r256 = (tm * ((N + 255) / 256) + ncu - 1) / ncu, r192 = (tm * ((N + 191) / 192) + ncu - 1) / ncu;
-  return r192 * 192 < r256 * 256;
+  return r192 * 85 < r256 * 100;
 }
 
 template <int EPI, int BK, int T>

@@ -20,6 +20,8 @@
 // The k-loop order is fixed and there is no split-K, so every output element is
 // computed the same way whatever M is and wherever its row sits: packed and
 // per-request projections agree bitwise.
+#include <atomic>
+
 #include "ditk_common.h"
 #include "gemm_l4_clobbers.h"
 
@@ -612,15 +614,19 @@ __device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __res
   }
 }
 
+// CUs of the current device, cached per device (callers on several host
+// threads may race to fill an entry; they store the same value)
 int cu_count() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
+  int c = cached[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
     int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    c = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    cached[dev].store(c, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return c;
 }
 template <int EPI, int FI>
 int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
     const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ W, int64_t ldw,
     const float* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K,
     const bf16_t* R, int64_t ldr, const float* __restrict__ gate, int64_t gate_stride,
-    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m) {
+    const int32_t* __restrict__ cu, int nseg, int tiles_m, int tiles_n, int group_m, int row_base) {
   using S = Stages<BK, T>;
   constexpr int GBM = S::GBM, GBN = S::GBN, GW = S::GW, WTM = S::WTM, WTN = S::WTN;
   constexpr int CPRW = S::CPRW, RPG = S::RPG, NSTAGE = S::NSTAGE, DPW_A = S::DPW_A, DPW_W = S::DPW_W;
@@ -315,8 +315,8 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
   bool one_seg = true;
   f32x4_t g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
   if (EPI == EPI_GATE_RES) {
-    seg_lo = find_segment(cu, nseg, m0 + a_row0);
-    one_seg = seg_lo == find_segment(cu, nseg, min(m0 + a_row0 + WTM, M) - 1);
+    seg_lo = find_segment(cu, nseg, row_base + m0 + a_row0);
+    one_seg = seg_lo == find_segment(cu, nseg, row_base + min(m0 + a_row0 + WTM, M) - 1);
     if (one_seg && n < N) {
       const float* gp = gate + (int64_t)seg_lo * gate_stride + n;
       g0 = *reinterpret_cast<const f32x4_t*>(gp);
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(Tile<T>::WM * Tile<T>::WN * 64, Tile<T>::WAVES_PER_
         if (EPI == EPI_GATE_RES) {
           f32x4_t h0 = g0, h1 = g1;
           if (!one_seg) {
-            const float* gp = gate + (int64_t)find_segment(cu, nseg, m) * gate_stride + n;
+            const float* gp = gate + (int64_t)find_segment(cu, nseg, row_base + m) * gate_stride + n;
             h0 = *reinterpret_cast<const f32x4_t*>(gp);
             h1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
           }
@@ -666,10 +666,26 @@ bool use_w192(int M, int N) {
   return r192 * 85 < r256 * 100;
 }
 
+// The rows of a short last 256-row tile, when leaving them to the small-tile
+// kernel (a second launch right after) saves the persistent kernel a round of
+// tiles: a 256-row tile costs the same however few of its rows are real, while
+// the small tiles (64 x 128) of the leftover rows take a fraction of a round.
+// E.g. M = 54560 = 213 * 256 + 32 and N = 3072: 2568 tiles = 11 rounds of 256
+// CUs, of which the last holds 8 tiles; 2556 tiles = 10 rounds plus the 32 rows
+// (Wan2.2-5B ffn-down 3.89 -> 3.56 ms, N = K = 3072 -8%, qkv -3%).  Every row is
+// computed the same way by either kernel, so the split changes no result.
+int l4_tail_rows(int M, int N, int gbn) {
+  const int64_t tm = (M + 255) / 256, rem = M % 256;
+  if (rem == 0 || tm < 2) return 0;
+  const int64_t tn = (N + gbn - 1) / gbn, ncu = std::max(8, cu_count() / 8 * 8);
+  const int64_t r_all = (tm * tn + ncu - 1) / ncu, r_main = ((tm - 1) * tn + ncu - 1) / ncu;
+  return r_main < r_all ? (int)rem : 0;
+}
+
 template <int EPI, int BK, int T>
 int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C,
                 int64_t ldc, int M, int N, int K, const void* R, int64_t ldr, const float* gate,
-                int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream) {
+                int64_t gate_stride, const int32_t* cu, int nseg, hipStream_t stream, int row_base = 0) {
   using S = Stages<BK, T>;
   const int tiles_m = (M + S::GBM - 1) / S::GBM, tiles_n = (N + S::GBN - 1) / S::GBN;
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
@@ -677,7 +693,7 @@ int launch_tile(const void* A, int64_t lda, const void* W, int64_t ldw, const fl
   DITK_REQUIRE(nblocks < (1ll << 31), "ditk_gemm: grid too large");
   gemm_kernel<EPI, BK, T><<<(unsigned)nblocks, S::GW * 64, 0, stream>>>(
       (const bf16_t*)A, lda, (const bf16_t*)W, ldw, bias, C, ldc, M, N, K, (const bf16_t*)R, ldr, gate,
-      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n));
+      gate_stride, cu, nseg, tiles_m, tiles_n, gemm_group_m(K, tiles_n), row_base);
   return ditk_check_launch("ditk_gemm");
 }
 
@@ -698,11 +714,21 @@ int launch(const void* A, int64_t lda, const void* W, int64_t ldw, const float* 
     return launch_tile<EPI, BK, TILE_SMALL>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
   // the large-tile kernel's epilogue addresses a wave tile's rows by 32-bit offsets
   const bool l4_strides = ldc < (1 << 22) && ldr < (1 << 22);
-  if (EPI != EPI_F32 && K % 64 == 0 && l4_strides && use_w192(M, N))
-    return launch_l4<EPI, 6>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
-  if (EPI != EPI_F32 && l4_strides && use_l4(N, K, EPI))
-    return launch_l4<EPI, 8>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
-  return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  const int fi = EPI == EPI_F32 || !l4_strides ? 0
+                 : K % 64 == 0 && use_w192(M, N) ? 6
+                 : use_l4(N, K, EPI)             ? 8
+                                                 : 0;
+  if (fi == 0)
+    return launch_tile<EPI, BK, TILE_LARGE>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  const int tail = l4_tail_rows(M, N, fi * 32);
+  const int Mm = M - tail;
+  const int rc = fi == 6 ? launch_l4<EPI, 6>(A, lda, W, ldw, bias, C, ldc, Mm, N, K, R, ldr, gate, gate_stride, cu, nseg, stream)
+                         : launch_l4<EPI, 8>(A, lda, W, ldw, bias, C, ldc, Mm, N, K, R, ldr, gate, gate_stride, cu, nseg, stream);
+  if (rc != 0 || tail == 0) return rc;
+  return launch_tile<EPI, BK, TILE_SMALL>(static_cast<const bf16_t*>(A) + (int64_t)Mm * lda, lda, W, ldw, bias,
+                                          static_cast<bf16_t*>(C) + (int64_t)Mm * ldc, ldc, tail, N, K,
+                                          R ? static_cast<const bf16_t*>(R) + (int64_t)Mm * ldr : nullptr, ldr, gate,
+                                          gate_stride, cu, nseg, stream, Mm);
 }
 
 template <int EPI>

@@ -136,6 +136,46 @@ def test_gemm_persistent_tiles_agree(epi):
         assert torch.equal(full[lo:hi], run(lo, hi)), (epi, lo, hi)
 
 
+@pytest.mark.parametrize("epi", ["bias", "res", "gate_res", "gelu"])
+def test_gemm_short_tile_row_split_agrees(epi):
+    """M = 10792 = 42 x 256 + 40, N = 4608, K = 1536: 43 x 18 = 774 large tiles
+    are 4 rounds of 256 CUs but 42 x 18 = 756 are 3, so the 40 rows of the last
+    tile row go to the small-tile kernel in a second launch (rows offset into the
+    gated residual's segments: a segment ends 22 rows into them).  The same rows
+    inside an 11008-row product (43 whole tile rows, one launch) are equal
+    bitwise, and the product is close to an fp32 reference."""
+    ops = _ops()
+    M, N, K, M2 = 10792, 4608, 1536, 11008
+    a = randn((M2, K), 60).to(DEV, torch.bfloat16)
+    w = randn((N, K), 61, 0.02).to(DEV, torch.bfloat16)
+    b = randn((N,), 62).to(DEV)
+    r = randn((M2, N), 63).to(DEV, torch.bfloat16)
+    gate = randn((4, N), 64).to(DEV)
+    cut = [0, 5000, 10774, M, M2]
+
+    def run(m):
+        kw = {}
+        if epi == "gate_res":
+            nseg = 3 if m == M else 4
+            kw = dict(residual=r[:m].contiguous(), gate=gate[:nseg], segments=_seg(cut[:nseg + 1]))
+        elif epi == "res":
+            kw = dict(residual=r[:m].contiguous())
+        return ops.linear(a[:m].contiguous(), w, b, epi, **kw)
+
+    y = run(M)
+    assert torch.equal(y, run(M2)[:M]), epi
+    rows = torch.arange(M - 300, M, device=DEV)
+    ref = a[rows].float() @ w.float().t() + b
+    if epi == "gelu":
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    elif epi == "res":
+        ref = r[rows].float() + ref.bfloat16().float()
+    elif epi == "gate_res":
+        seg = torch.bucketize(rows, torch.tensor(cut[1:4], device=DEV), right=True)
+        ref = r[rows].float() + ref.bfloat16().float() * gate[seg]
+    assert_close(y[rows].float(), ref, 0.999, 1e-2, f"split {epi}")
+
+
 def test_gemm_stage_depths_agree():
     """K % 64 == 0 runs 64-k LDS stages, otherwise 32-k stages; the MFMA k order is
     the same, so zero-padding K by 32 (forcing the 32-k path) changes no bit."""

@@ -81,6 +81,8 @@ int ditk_qk_norm_rope_out(const void* q, int64_t ldq, const void* k, int64_t ldk
  *   0 bias, 1 GELU-tanh, 2 gated residual R + bf16(y) * gate[seg] (fp32 math),
  *   3 residual R + bf16(y), 4 fp32 output, 5 SiLU.
  * C may alias R.  No split-K: results do not depend on M or on row position.
+ * One kernel launch on `stream`, or two when a short last 256-row tile row is
+ * left to a small-tile launch (rows are split, never k).
  * K % 32 == 0, N % 8 == 0; A, W, C, R and bias (fp32 [N] or NULL) 16-byte aligned.
  * Replaces: nn.Linear projections of the Wan block (to_q/to_k/to_v/to_out,
  *   ffn.net.0/ffn.net.2) — transformer_wan.py:50-69,154-155; block.py:285,293;

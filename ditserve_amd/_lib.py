@@ -28,6 +28,9 @@ SIGNATURES = {
                                       _P, c_float, c_int, _P, _P, c_int, _P, _P, c_int, c_int, c_int, _P]),
     "ditk_gemm": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int, c_int, c_int, c_int, _P, c_int64,
                           _P, c_int64, _P, c_int, _P]),
+    "ditk_gemm_pair": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int, _P, c_int64, _P, c_int64, _P, c_int,
+                               _P, c_int64, _P, c_int64, _P, _P, c_int64, c_int, _P, c_int64, _P, c_int64, _P, c_int,
+                               c_int, c_int, c_int, _P]),
     "ditk_vt_columns": (c_int64, [c_int64, c_int]),
     "ditk_transpose_v": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, _P, c_int, _P]),
     "ditk_flash_attn_varlen": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P,

@@ -445,6 +445,44 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel_l4(
                      tiles_n, group_m);
 }
 
+// One product of a paired launch (see gemm_kernel_l4_pair).
+struct L4Prob {
+  const bf16_t* A;
+  int64_t lda;
+  const bf16_t* W;
+  int64_t ldw;
+  const float* bias;
+  void* C;
+  int64_t ldc;
+  const bf16_t* R;
+  int64_t ldr;
+  const float* gate;
+  int64_t gate_stride;
+  const int32_t* cu;
+  int nseg, M, tiles_m, group_m;
+};
+
+// Two products of the same N, K and epilogue (their own inputs, weights, bias,
+// residual, gate and segments) in one persistent launch: the tile list is the
+// first product's tiles, then the second's, taken per XCD as gemm_kernel_l4
+// takes one product's.  Each tile is computed exactly as a launch of its own
+// product would compute it.
+template <int EPI, int FI>
+__global__ __launch_bounds__(256, 1) void gemm_kernel_l4_pair(L4Prob p0, L4Prob p1, int N, int K, int tiles_n) {
+  __shared__ u32x4_t lds[L4<FI>::LDS_BYTES / 16];
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int t0 = p0.tiles_m * tiles_n, ntiles = t0 + p1.tiles_m * tiles_n, per_xcd = (ntiles + 7) / 8;
+  const int tlo = (b & 7) * per_xcd, thi = min(tlo + per_xcd, ntiles);
+  for (int L = tlo + (b >> 3); L < thi; L += nb >> 3) {
+    const bool s = L >= t0;  // wave-uniform: the fields below are scalar selects
+    l4_tile<EPI, FI>(lds, s ? L - t0 : L, s ? p1.A : p0.A, s ? p1.lda : p0.lda, s ? p1.W : p0.W,
+                     s ? p1.ldw : p0.ldw, s ? p1.bias : p0.bias, s ? p1.C : p0.C, s ? p1.ldc : p0.ldc,
+                     s ? p1.M : p0.M, N, K, s ? p1.R : p0.R, s ? p1.ldr : p0.ldr, s ? p1.gate : p0.gate,
+                     s ? p1.gate_stride : p0.gate_stride, s ? p1.cu : p0.cu, s ? p1.nseg : p0.nseg,
+                     s ? p1.tiles_m : p0.tiles_m, tiles_n, s ? p1.group_m : p0.group_m);
+  }
+}
+
 template <int EPI, int FI>
 __device__ __forceinline__ void l4_tile(u32x4_t* lds, int L, const bf16_t* __restrict__ A, int64_t lda,
                                         const bf16_t* __restrict__ W, int64_t ldw, const float* __restrict__ bias,
@@ -642,6 +680,18 @@ int launch_l4(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
   return ditk_check_launch("ditk_gemm");
 }
 
+template <int EPI>
+int launch_l4_pair(L4Prob p0, L4Prob p1, int N, int K, hipStream_t stream) {
+  const int tiles_n = (N + 255) / 256;
+  p0.tiles_m = (p0.M + 255) / 256;
+  p1.tiles_m = (p1.M + 255) / 256;
+  p0.group_m = p1.group_m = gemm_group_m(K, tiles_n);
+  const int64_t tiles = (int64_t)(p0.tiles_m + p1.tiles_m) * tiles_n;
+  const int64_t nblocks = std::min<int64_t>((tiles + 7) / 8 * 8, std::max(8, cu_count() / 8 * 8));
+  gemm_kernel_l4_pair<EPI, 8><<<(unsigned)nblocks, 256, 0, stream>>>(p0, p1, N, K, tiles_n);
+  return ditk_check_launch("ditk_gemm_pair");
+}
+
 // The one-wave-per-SIMD kernel where it measured faster than gemm_kernel's large
 // tiles (same box, Wan2.1 block shapes at M = 65520): N >= 3072 or K >= 4096
 // (qkv -3.4%, ffn-up -2.9%, ffn-down -4.7%, N = 3072 SiLU -3.3%), and, since its
@@ -680,6 +730,22 @@ int l4_tail_rows(int M, int N, int gbn) {
   const int64_t tn = (N + gbn - 1) / gbn, ncu = std::max(8, cu_count() / 8 * 8);
   const int64_t r_all = (tm * tn + ncu - 1) / ncu, r_main = ((tm - 1) * tn + ncu - 1) / ncu;
   return r_main < r_all ? (int)rem : 0;
+}
+
+// A paired launch (256 x 256 tiles) when its rounds of tiles cost no more than
+// the larger product alone (its own tile width) plus 0.4 of a round for the
+// smaller one's separate launch (measured: 666 rows at N = 1536, K = 1536 and
+// 6144 take 30-50 us beside 52-134 us rounds).  SD3.5's gated-residual
+// projections, 8192 image + 666 text rows at N = 1536: 192 + 18 tiles are one
+// round, against one 192-wide round plus a text launch.  qkv (N = 4608) and the
+// feed-forward input (N = 6144) do not pair: the text tiles would add a round.
+bool pair_pays(int M0, int M1, int N) {
+  const int64_t ncu = std::max(8, cu_count() / 8 * 8), tn = (N + 255) / 256;
+  const int64_t big = std::max(M0, M1), t_all = ((int64_t)(M0 + 255) / 256 + (M1 + 255) / 256) * tn;
+  const int64_t tb = (big + 255) / 256;
+  const int64_t r_pair = (t_all + ncu - 1) / ncu, r256 = (tb * tn + ncu - 1) / ncu,
+                r192 = (tb * ((N + 191) / 192) + ncu - 1) / ncu;
+  return r_pair * 100 <= std::min(r256 * 100, r192 * 85) + 40;
 }
 
 template <int EPI, int BK, int T>
@@ -743,10 +809,10 @@ int launch_k(const void* A, int64_t lda, const void* W, int64_t ldw, const float
 
 }  // namespace
 
-DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
-                          void* C, int64_t ldc, int M, int N, int K, int epilogue, const void* R,
-                          int64_t ldr, const float* gate, int64_t gate_stride,
-                          const int32_t* cu_seqlens, int nseg, hipStream_t stream) {
+namespace {
+int gemm_validate(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+                  int M, int N, int K, int epilogue, const void* R, int64_t ldr, const float* gate,
+                  int64_t gate_stride, const int32_t* cu_seqlens, int nseg) {
   DITK_REQUIRE(A && W && C, "ditk_gemm: null operand");
   DITK_REQUIRE(M >= 0 && N > 0 && K > 0, "ditk_gemm: bad shape M=%d N=%d K=%d", M, N, K);
   DITK_REQUIRE(K % 32 == 0, "ditk_gemm: K=%d must be a multiple of 32", K);
@@ -767,6 +833,12 @@ DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw
                "ditk_gemm: gate rows must be 16-byte aligned");
   DITK_REQUIRE(epilogue != EPI_GATE_RES || (gate && cu_seqlens && nseg > 0),
                "ditk_gemm: gated epilogue needs gate and cu_seqlens");
+  return 0;
+}
+
+int gemm_run(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+             int M, int N, int K, int epilogue, const void* R, int64_t ldr, const float* gate,
+             int64_t gate_stride, const int32_t* cu_seqlens, int nseg, hipStream_t stream) {
   if (M == 0) return 0;
   switch (epilogue) {
     case EPI_BIAS: return launch_k<EPI_BIAS>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu_seqlens, nseg, stream);
@@ -776,4 +848,51 @@ DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw
     case EPI_F32: return launch_k<EPI_F32>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu_seqlens, nseg, stream);
     default: return launch_k<EPI_SILU>(A, lda, W, ldw, bias, C, ldc, M, N, K, R, ldr, gate, gate_stride, cu_seqlens, nseg, stream);
   }
+}
+}  // namespace
+
+DITK_EXPORT int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
+                          void* C, int64_t ldc, int M, int N, int K, int epilogue, const void* R,
+                          int64_t ldr, const float* gate, int64_t gate_stride,
+                          const int32_t* cu_seqlens, int nseg, hipStream_t stream) {
+  if (int rc = gemm_validate(A, lda, W, ldw, bias, C, ldc, M, N, K, epilogue, R, ldr, gate, gate_stride,
+                             cu_seqlens, nseg))
+    return rc;
+  return gemm_run(A, lda, W, ldw, bias, C, ldc, M, N, K, epilogue, R, ldr, gate, gate_stride, cu_seqlens, nseg,
+                  stream);
+}
+
+DITK_EXPORT int ditk_gemm_pair(const void* A0, int64_t lda0, const void* W0, int64_t ldw0, const float* bias0,
+                               void* C0, int64_t ldc0, int M0, const void* R0, int64_t ldr0, const float* gate0,
+                               int64_t gate_stride0, const int32_t* cu_seqlens0, int nseg0, const void* A1,
+                               int64_t lda1, const void* W1, int64_t ldw1, const float* bias1, void* C1,
+                               int64_t ldc1, int M1, const void* R1, int64_t ldr1, const float* gate1,
+                               int64_t gate_stride1, const int32_t* cu_seqlens1, int nseg1, int N, int K,
+                               int epilogue, hipStream_t stream) {
+  if (int rc = gemm_validate(A0, lda0, W0, ldw0, bias0, C0, ldc0, M0, N, K, epilogue, R0, ldr0, gate0,
+                             gate_stride0, cu_seqlens0, nseg0))
+    return rc;
+  if (int rc = gemm_validate(A1, lda1, W1, ldw1, bias1, C1, ldc1, M1, N, K, epilogue, R1, ldr1, gate1,
+                             gate_stride1, cu_seqlens1, nseg1))
+    return rc;
+  // the large-tile kernel addresses a wave tile's output and residual rows by 32-bit offsets
+  const bool strides = ldc0 < (1 << 22) && ldr0 < (1 << 22) && ldc1 < (1 << 22) && ldr1 < (1 << 22);
+  if (M0 > 0 && M1 > 0 && epilogue != EPI_F32 && K % 64 == 0 && strides && pair_pays(M0, M1, N)) {
+    const L4Prob p0{(const bf16_t*)A0, lda0, (const bf16_t*)W0, ldw0, bias0, C0, ldc0, (const bf16_t*)R0, ldr0,
+                    gate0, gate_stride0, cu_seqlens0, nseg0, M0, 0, 0};
+    const L4Prob p1{(const bf16_t*)A1, lda1, (const bf16_t*)W1, ldw1, bias1, C1, ldc1, (const bf16_t*)R1, ldr1,
+                    gate1, gate_stride1, cu_seqlens1, nseg1, M1, 0, 0};
+    switch (epilogue) {
+      case EPI_BIAS: return launch_l4_pair<EPI_BIAS>(p0, p1, N, K, stream);
+      case EPI_GELU: return launch_l4_pair<EPI_GELU>(p0, p1, N, K, stream);
+      case EPI_GATE_RES: return launch_l4_pair<EPI_GATE_RES>(p0, p1, N, K, stream);
+      case EPI_RES: return launch_l4_pair<EPI_RES>(p0, p1, N, K, stream);
+      default: return launch_l4_pair<EPI_SILU>(p0, p1, N, K, stream);
+    }
+  }
+  if (int rc = gemm_run(A0, lda0, W0, ldw0, bias0, C0, ldc0, M0, N, K, epilogue, R0, ldr0, gate0, gate_stride0,
+                        cu_seqlens0, nseg0, stream))
+    return rc;
+  return gemm_run(A1, lda1, W1, ldw1, bias1, C1, ldc1, M1, N, K, epilogue, R1, ldr1, gate1, gate_stride1,
+                  cu_seqlens1, nseg1, stream);
 }

@@ -242,12 +242,9 @@ def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None, o
 # GEMM
 # ---------------------------------------------------------------------------
 
-def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=None, out=None):
-    """out = epilogue(x @ w.T + b) on MFMA.
-
-    x [M, K] bf16 (row view), w [N, K] bf16, b [N] fp32.  Epilogues: "bias",
-    "gelu" (GELU-tanh), "gate_res" (residual + bf16(y) * gate[seg]), "res"
-    (residual + bf16(y)), "f32" (fp32 output), "silu"."""
+def _linear_args(x, w, b, epilogue, residual, gate, segments, out):
+    """Checks one product's operands; returns (out, ditk_gemm's operand arguments
+    without the epilogue and stream, N, K)."""
     _check(x, "x", _BF16, 2)
     _check(w, "w", _BF16, 2)
     M, K = x.shape
@@ -259,7 +256,8 @@ def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=Non
         _check(b, "bias", torch.float32, 1)
         if b.shape[0] != N:
             raise ValueError("bias size mismatch")
-    epi = EPILOGUES[epilogue]
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"unknown epilogue {epilogue!r}")
     odt = torch.float32 if epilogue == "f32" else _BF16
     if out is None:
         out = torch.empty((M, N), dtype=odt, device=x.device)
@@ -281,9 +279,38 @@ def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=Non
         if gate.shape != (segments.nseg, N) or gate.stride(1) != 1 or gate.stride(0) % 4 or gate.data_ptr() % 16:
             raise ValueError(f"gate must be [{segments.nseg}, {N}] with unit column stride and 16-byte aligned rows")
         gate_stride, cu, nseg = gate.stride(0), segments.dev, segments.nseg
-    _lib.call("ditk_gemm", _ptr(x), lda, _ptr(w), ldw, _ptr(b), _ptr(out), out.stride(0), M, N, K, epi,
-              _ptr(residual), ldr, _ptr(gate), gate_stride, _ptr(cu), nseg, _stream())
+    return out, (_ptr(x), lda, _ptr(w), ldw, _ptr(b), _ptr(out), out.stride(0), M, _ptr(residual), ldr, _ptr(gate),
+                 gate_stride, _ptr(cu), nseg), N, K
+
+
+def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=None, out=None):
+    """out = epilogue(x @ w.T + b) on MFMA.
+
+    x [M, K] bf16 (row view), w [N, K] bf16, b [N] fp32.  Epilogues: "bias",
+    "gelu" (GELU-tanh), "gate_res" (residual + bf16(y) * gate[seg]), "res"
+    (residual + bf16(y)), "f32" (fp32 output), "silu"."""
+    out, a, N, K = _linear_args(x, w, b, epilogue, residual, gate, segments, out)
+    (xp, lda, wp, ldw, bp, op, ldc, M, rp, ldr, gp, gate_stride, cup, nseg) = a
+    _lib.call("ditk_gemm", xp, lda, wp, ldw, bp, op, ldc, M, N, K, EPILOGUES[epilogue], rp, ldr, gp, gate_stride,
+              cup, nseg, _stream())
     return out
+
+
+def linear_pair(p0, p1, epilogue="bias"):
+    """Two linear() products of the same N, K and epilogue (e.g. an SD3.5 block's
+    image and text projections), in one launch when their tiles fit the larger
+    one's rounds.  p0, p1: dicts of linear()'s arguments (x, w, and optionally b,
+    residual, gate, segments, out).  Returns (out0, out1), each bitwise what
+    linear() returns for it."""
+    def args(p):
+        return _linear_args(p["x"], p["w"], p.get("b"), epilogue, p.get("residual"), p.get("gate"),
+                            p.get("segments"), p.get("out"))
+    o0, a0, N0, K0 = args(p0)
+    o1, a1, N1, K1 = args(p1)
+    if (N0, K0) != (N1, K1):
+        raise ValueError(f"linear_pair needs one N and K (got {N0}x{K0} and {N1}x{K1})")
+    _lib.call("ditk_gemm_pair", *a0, *a1, N0, K0, EPILOGUES[epilogue], _stream())
+    return o0, o1
 
 
 # ---------------------------------------------------------------------------

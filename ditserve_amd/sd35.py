@@ -294,7 +294,13 @@ class SD35Transformer:
                 qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D], vt, seg_img, seg_txt,
                 seg_joint, cfg.heads, cfg.head_dim)
         with prof.region("gemm_out"):
-            h = ops.linear(a_img, *blk["out"], "gate_res", residual=h, gate=emb[:, 2 * D:3 * D], segments=seg_img)
+            img = dict(x=a_img, w=blk["out"][0], b=blk["out"][1], residual=h, gate=emb[:, 2 * D:3 * D],
+                       segments=seg_img)
+            if blk["last"]:
+                h = ops.linear(epilogue="gate_res", **img)
+            else:  # image and text output projections, one launch where that pays
+                h, c = ops.linear_pair(img, dict(x=a_txt, w=blk["out_t"][0], b=blk["out_t"][1], residual=c,
+                                                 gate=embc[:, 2 * D:3 * D], segments=seg_txt), "gate_res")
         if blk["dual"]:
             with prof.region("attn_dual"):
                 qkv2 = ops.linear(nh2, *blk["qkv2"])
@@ -303,13 +309,15 @@ class SD35Transformer:
         with prof.region("ffn"):
             n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)
             fx = ops.linear(n2, *blk["ff1"], "gelu")
-            ops.linear(fx, *blk["ff2"], "gate_res", residual=h, gate=emb[:, 5 * D:6 * D], segments=seg_img, out=h)
+            img = dict(x=fx, w=blk["ff2"][0], b=blk["ff2"][1], residual=h, gate=emb[:, 5 * D:6 * D],
+                       segments=seg_img, out=h)
             if blk["last"]:
+                ops.linear(epilogue="gate_res", **img)
                 return h, None
-            c = ops.linear(a_txt, *blk["out_t"], "gate_res", residual=c, gate=embc[:, 2 * D:3 * D], segments=seg_txt)
             n2c = ops.adaln(c, embc[:, 3 * D:4 * D], embc[:, 4 * D:5 * D], seg_txt, eps=eps)
             fc = ops.linear(n2c, *blk["ffc1"], "gelu")
-            ops.linear(fc, *blk["ffc2"], "gate_res", residual=c, gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c)
+            ops.linear_pair(img, dict(x=fc, w=blk["ffc2"][0], b=blk["ffc2"][1], residual=c,
+                                      gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c), "gate_res")
         return h, c
 
     # ------------------------------------------------------------------ forward

@@ -92,6 +92,22 @@ int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
               int M, int N, int K, int epilogue, const void* R, int64_t ldr, const float* gate,
               int64_t gate_stride, const int32_t* cu_seqlens, int nseg, ditk_stream_t stream);
 
+/*
+ * Two ditk_gemm products of the same N, K and epilogue, each with its own
+ * operands (suffix 0 and 1; arguments as ditk_gemm's), in one launch when their
+ * tiles fit the rounds of the larger one (else two launches).  Every row equals,
+ * bitwise, what ditk_gemm computes for it.
+ * Replaces: the image- and context-stream projections of one SD3.5 joint block,
+ *   issued back to back: attn.to_out / attn.to_add_out (sd35_batch.py:573-579)
+ *   and the second linear of ff / ff_context (sd35_batch.py:698,707).
+ */
+int ditk_gemm_pair(const void* A0, int64_t lda0, const void* W0, int64_t ldw0, const float* bias0, void* C0,
+                   int64_t ldc0, int M0, const void* R0, int64_t ldr0, const float* gate0, int64_t gate_stride0,
+                   const int32_t* cu_seqlens0, int nseg0, const void* A1, int64_t lda1, const void* W1,
+                   int64_t ldw1, const float* bias1, void* C1, int64_t ldc1, int M1, const void* R1, int64_t ldr1,
+                   const float* gate1, int64_t gate_stride1, const int32_t* cu_seqlens1, int nseg1, int N, int K,
+                   int epilogue, ditk_stream_t stream);
+
 /* Columns of the transposed-V buffer for Tk keys in nseg segments (upper bound). */
 int64_t ditk_vt_columns(int64_t Tk, int nseg);
 

@@ -176,6 +176,34 @@ def test_gemm_short_tile_row_split_agrees(epi):
     assert_close(y[rows].float(), ref, 0.999, 1e-2, f"split {epi}")
 
 
+@pytest.mark.parametrize("epi", ["gate_res", "bias", "gelu", "res"])
+@pytest.mark.parametrize("M0,M1,N,K", [(8192, 666, 1536, 1536),   # one launch: 192 + 18 tiles = one round
+                                       (666, 8192, 1536, 6144),   # the same, text first, long K
+                                       (8192, 666, 4608, 1536)])  # two launches: the text tiles add a round
+def test_gemm_pair_matches_separate(epi, M0, M1, N, K):
+    """ditk_gemm_pair (SD3.5's image and text projections of one block) returns,
+    bitwise, what two ditk_gemm calls return, in one launch or two; each product
+    keeps its own gate rows and segments (2 image, 2 text)."""
+    ops = _ops()
+
+    def prob(M, seed):
+        p = dict(x=randn((M, K), seed).to(DEV, torch.bfloat16), w=randn((N, K), seed + 1, 0.02).to(DEV, torch.bfloat16),
+                 b=randn((N,), seed + 2).to(DEV))
+        if epi in ("gate_res", "res"):
+            p["residual"] = randn((M, N), seed + 3).to(DEV, torch.bfloat16)
+        if epi == "gate_res":
+            p["gate"] = randn((2, N), seed + 4).to(DEV)
+            p["segments"] = _seg([0, M // 2 + 7, M])
+        return p
+
+    p0, p1 = prob(M0, 70), prob(M1, 80)
+    y0, y1 = ops.linear_pair(p0, p1, epi)
+    assert torch.equal(y0, ops.linear(epilogue=epi, **p0)), "first product"
+    assert torch.equal(y1, ops.linear(epilogue=epi, **p1)), "second product"
+    with pytest.raises(ValueError):
+        ops.linear_pair(p0, dict(x=p1["x"][:, :K - 32].contiguous(), w=p1["w"][:, :K - 32].contiguous()), epi)
+
+
 def test_gemm_stage_depths_agree():
     """K % 64 == 0 runs 64-k LDS stages, otherwise 32-k stages; the MFMA k order is
     the same, so zero-padding K by 32 (forcing the 32-k path) changes no bit."""

@@ -94,9 +94,10 @@ int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
 
 /*
  * Two ditk_gemm products of the same N, K and epilogue, each with its own
- * operands (suffix 0 and 1; arguments as ditk_gemm's), in one launch when their
- * tiles fit the rounds of the larger one (else two launches).  Every row equals,
- * bitwise, what ditk_gemm computes for it.
+ * operands (suffix 0 and 1; arguments as ditk_gemm's), in one launch when the
+ * two tile lists together take no more rounds of the GPU's CUs than the larger
+ * product alone, give or take 0.4 of a round (else two launches).  Every row
+ * equals, bitwise, what ditk_gemm computes for it.
  * Replaces: the image- and context-stream projections of one SD3.5 joint block,
  *   issued back to back: attn.to_out / attn.to_add_out (sd35_batch.py:573-579)
  *   and the second linear of ff / ff_context (sd35_batch.py:698,707).

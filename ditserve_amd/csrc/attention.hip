@@ -297,8 +297,13 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
                                                           int nseg, const bf16_t* __restrict__ Vb,
                                                           const int32_t* __restrict__ cu_a,
                                                           const int32_t* __restrict__ cu_b) {
-  constexpr int PITCH = HD + 2;  // u16 pitch: odd word stride spreads column reads over banks
-  __shared__ bf16_t tile[BN * PITCH];
+  // LDS tile of 32-bit words: word (d, p) holds keys 2p (low half) and 2p + 1 of
+  // head dim d, so a 16-byte read gives 8 consecutive keys of one d.  Row pitch 36
+  // words (16-byte aligned rows); key-pair groups of 4 rotated by d / 8 so the
+  // writes of one wave (16 d-chunks x 4 key pairs) fall two lanes per bank.
+  constexpr int PW = 36;
+  __shared__ uint32_t tile[HD * PW];
+  auto col = [](int d, int p) { return (p + 4 * ((d >> 3) & 7)) & 31; };
   int t = blockIdx.x;
   const int head = blockIdx.y;
   const int seg = locate_tile(cu, nseg, BN, t);
@@ -308,8 +313,8 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
   const int col0 = padded_key_start(cu, seg) + t * BN;
   const bf16_t* Vh = V + (int64_t)head * HD;
   constexpr int CH = HD / 8;
-  for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
-    int r = idx / CH, ch = idx % CH;
+  // row r of this tile (zero past the segment end)
+  auto load_row = [&](int r, int ch) {
     u32x4_t v = u32x4_t{0, 0, 0, 0};
     if (k0 + r < k_end) {
       if (cu_a != nullptr) {
@@ -321,20 +326,24 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
         v = *reinterpret_cast<const u32x4_t*>(Vh + (int64_t)(k0 + r) * ldv + ch * 8);
       }
     }
+    return v;
+  };
+  // 16-byte chunk ch of rows 2p and 2p + 1 (a wave reads CH chunks of 64 / CH rows pairs)
+  for (int idx = threadIdx.x; idx < (BN / 2) * CH; idx += 256) {
+    const int ch = idx % CH, p = idx / CH;
+    const u32x4_t lo = load_row(2 * p, ch), hi = load_row(2 * p + 1, ch);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      tile[r * PITCH + ch * 8 + 2 * i] = (bf16_t)(v[i] & 0xffffu);
-      tile[r * PITCH + ch * 8 + 2 * i + 1] = (bf16_t)(v[i] >> 16);
+      const int d = ch * 8 + 2 * i;
+      tile[d * PW + col(d, p)] = (lo[i] & 0xffffu) | (hi[i] << 16);
+      tile[(d + 1) * PW + col(d + 1, p)] = (lo[i] >> 16) | (hi[i] & 0xffff0000u);
     }
   }
   __syncthreads();
   bf16_t* out = Vt + (int64_t)head * vt_hs + col0;
   for (int idx = threadIdx.x; idx < HD * (BN / 8); idx += 256) {
-    int d = idx >> 3, kc = idx & 7;
-    u32x4_t w;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)tile[(kc * 8 + 2 * i) * PITCH + d] | ((uint32_t)tile[(kc * 8 + 2 * i + 1) * PITCH + d] << 16);
+    const int d = idx >> 3, kc = idx & 7;  // keys 8 kc .. 8 kc + 7 = key pairs 4 kc .. 4 kc + 3
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(&tile[d * PW + col(d, 4 * kc)]);
     *reinterpret_cast<u32x4_t*>(out + (int64_t)d * vt_ld + kc * 8) = w;
   }
 }

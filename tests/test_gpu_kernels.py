@@ -629,6 +629,29 @@ def test_joint_gather_scatter_roundtrip():
     assert torch.equal(img2, img) and torch.equal(txt2, txt)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_transpose_v_layout(hd):
+    """Vt[h, d, pk_m + j] = V[cu[m] + j, h * hd + d] for the rows of segment m,
+    zero up to its 64-padded end (pk_m = the padded lengths of the segments
+    before it); V is a column slice of a fused QKV row (ragged and empty
+    segments, one key, a tile boundary)."""
+    ops = _ops()
+    H, cu = 3, [0, 1, 130, 130, 333, 397]
+    T = cu[-1]
+    qkv = randn((T, 3 * H * hd), 90).to(DEV, torch.bfloat16)
+    v = qkv[:, 2 * H * hd:]
+    vt = ops.transpose_v(v, H, hd, _seg(cu)).cpu()
+    vc = v.cpu()
+    pk = 0
+    for m in range(len(cu) - 1):
+        n = cu[m + 1] - cu[m]
+        padded = (n + 63) // 64 * 64
+        want = torch.zeros((H, hd, padded), dtype=torch.bfloat16)
+        want[:, :, :n] = vc[cu[m]:cu[m + 1]].reshape(n, H, hd).permute(1, 2, 0)
+        assert torch.equal(vt[:, :, pk:pk + padded], want), (hd, m)
+        pk += padded
+
+
 def test_invalid_arguments_raise_before_launch():
     ops = _ops()
     from ditserve_amd._lib import DitkError

@@ -351,6 +351,133 @@ def test_sd35_joint_block_one_image_one_text_token_uniform():
     assert torch.allclose(oh, h2, atol=1e-10) and torch.allclose(oc_, c2, atol=1e-10)
 
 
+def _one_token_inputs(seed):
+    h = torch.randn(1, 128, generator=g(seed), dtype=D64)
+    c = torch.randn(1, 128, generator=g(seed + 1), dtype=D64)
+    temb = torch.randn(128, generator=g(seed + 2), dtype=D64) * 4.0  # gates of order 1
+    return h, c, temb
+
+
+def _ff(p, pre, x):
+    return _lin(p, f"{pre}.net.2", F.gelu(_lin(p, f"{pre}.net.0.proj", x), approximate="tanh"))
+
+
+def _ln128(x):
+    return F.layer_norm(x, (128,), eps=1e-6)
+
+
+def test_sd35_dual_block_one_image_one_text_token():
+    """A dual-attention block (sd35_batch.py:647-708 with use_dual_attention): norm1's
+    9-chunk AdaLN-Zero is (shift, scale, gate, shift_mlp, scale_mlp, gate_mlp, shift2,
+    scale2, gate2) (sd35_batch.py:351-363); normed2 = LN(h)(1 + scale2) + shift2 of the
+    PRE-attention h; attn2 over one image token is to_out(to_v(normed2)) whatever its q/k;
+    its term gate2 · attn2 is added after the joint residual and before the image FFN,
+    whose LayerNorm reads the updated h (sd35_batch.py:681-699)."""
+    _, p = _tiny_sd35(dual=(0,))
+    pre = "transformer_blocks.0"
+    p = _zero_qk(_zero_qk(p, f"{pre}.attn"), f"{pre}.attn", "add_q_proj", "add_k_proj")
+    ocfg = dict(heads=2, eps=1e-6, layers=2, dual_layers=(0,))
+    h, c, temb = _one_token_inputs(40)
+    oh, oc_ = osd.joint_block(p, 0, h, c, temb, ocfg)
+    sh, sc, ga, shm, scm, gam, sh2, sc2, ga2 = _lin(p, f"{pre}.norm1.linear", F.silu(temb)).reshape(9, 128).unbind(0)
+    csh, csc, cga, cshm, cscm, cgam = _lin(p, f"{pre}.norm1_context.linear", F.silu(temb)).reshape(6, 128).unbind(0)
+    ni, nt = _ln128(h) * (1 + sc) + sh, _ln128(c) * (1 + csc) + csh
+    ni2 = _ln128(h) * (1 + sc2) + sh2
+    mean_v = 0.5 * (_lin(p, f"{pre}.attn.to_v", ni) + _lin(p, f"{pre}.attn.add_v_proj", nt))
+    h1 = h + ga * _lin(p, f"{pre}.attn.to_out.0", mean_v)
+    h1 = h1 + ga2 * _lin(p, f"{pre}.attn2.to_out.0", _lin(p, f"{pre}.attn2.to_v", ni2))
+    h2 = h1 + gam * _ff(p, f"{pre}.ff", _ln128(h1) * (1 + scm) + shm)
+    c1 = c + cga * _lin(p, f"{pre}.attn.to_add_out", mean_v)
+    c2 = c1 + cgam * _ff(p, f"{pre}.ff_context", _ln128(c1) * (1 + cscm) + cshm)
+    assert torch.allclose(oh, h2, atol=1e-10) and torch.allclose(oc_, c2, atol=1e-10)
+
+
+def test_sd35_last_block_one_image_one_text_token():
+    """The last (context_pre_only) block: the text goes through AdaLN-Continuous,
+    (scale, shift) = chunk(2) (sd35_batch.py:379-393, 624-628), into the joint attention,
+    which returns no text output; only the image stream gets its gated residual and FFN,
+    and the block returns no text (sd35_batch.py:666-708)."""
+    _, p = _tiny_sd35()
+    pre = "transformer_blocks.1"
+    p = _zero_qk(_zero_qk(p, f"{pre}.attn"), f"{pre}.attn", "add_q_proj", "add_k_proj")
+    ocfg = dict(heads=2, eps=1e-6, layers=2, dual_layers=())
+    h, c, temb = _one_token_inputs(43)
+    oh, oc_ = osd.joint_block(p, 1, h, c, temb, ocfg)
+    assert oc_ is None
+    sh, sc, ga, shm, scm, gam = _lin(p, f"{pre}.norm1.linear", F.silu(temb)).reshape(6, 128).unbind(0)
+    cscale, cshift = _lin(p, f"{pre}.norm1_context.linear", F.silu(temb)).reshape(2, 128).unbind(0)
+    ni, nt = _ln128(h) * (1 + sc) + sh, _ln128(c) * (1 + cscale) + cshift
+    mean_v = 0.5 * (_lin(p, f"{pre}.attn.to_v", ni) + _lin(p, f"{pre}.attn.add_v_proj", nt))
+    h1 = h + ga * _lin(p, f"{pre}.attn.to_out.0", mean_v)
+    h2 = h1 + gam * _ff(p, f"{pre}.ff", _ln128(h1) * (1 + scm) + shm)
+    assert torch.allclose(oh, h2, atol=1e-10)
+
+
+def _joint_block_variant(dual_gate_chunk=8, normed2_from_pre=True, dual_before_ffn=True, last_text="continuous"):
+    """The oracle's joint block written out with switches for plausible mistakes:
+    the dual gate read from another chunk (2 = gate_msa, 5 = gate_mlp), normed2 taken
+    from the post-attention h, the dual term added after the FFN, and the last block's
+    text normalised in AdaLN-Zero's chunk order (shift first) or not modulated at all."""
+    def fn(p, i, h, c, temb, cfg, attn=oc.sdpa):
+        pre = f"transformer_blocks.{i}"
+        heads, eps = cfg["heads"], cfg["eps"]
+        pre_only, dual = i == cfg["layers"] - 1, i in cfg["dual_layers"]
+        d = h.shape[-1]
+        ch = oc.linear(oc.silu(temb), p[f"{pre}.norm1.linear.weight"], p[f"{pre}.norm1.linear.bias"]).reshape(-1, d)
+        normed = oc.layer_norm(h, eps) * (1.0 + ch[1]) + ch[0]
+        cc = oc.linear(oc.silu(temb), p[f"{pre}.norm1_context.linear.weight"],
+                       p[f"{pre}.norm1_context.linear.bias"]).reshape(-1, d)
+        if pre_only:
+            if last_text == "continuous":
+                nc = oc.layer_norm(c, eps) * (1.0 + cc[0]) + cc[1]
+            elif last_text == "zero_order":
+                nc = oc.layer_norm(c, eps) * (1.0 + cc[1]) + cc[0]
+            else:
+                nc = oc.layer_norm(c, eps)
+        else:
+            nc = oc.layer_norm(c, eps) * (1.0 + cc[1]) + cc[0]
+        img, txt = osd.joint_attention(p, f"{pre}.attn", normed, nc, heads, pre_only, eps, attn)
+        h_pre = h
+        h = h + ch[2] * img
+
+        def dual_term(hh):
+            src = h_pre if normed2_from_pre else hh
+            n2 = oc.layer_norm(src, eps) * (1.0 + ch[7]) + ch[6]
+            return ch[dual_gate_chunk] * osd.self_attention(p, f"{pre}.attn2", n2, heads, eps, attn)
+        if dual and dual_before_ffn:
+            h = h + dual_term(h)
+        h = h + ch[5] * osd.ffn(p, f"{pre}.ff", oc.layer_norm(h, eps) * (1.0 + ch[4]) + ch[3])
+        if dual and not dual_before_ffn:
+            h = h + dual_term(h)
+        if pre_only:
+            return h, None
+        c = c + cc[2] * txt
+        c = c + cc[5] * osd.ffn(p, f"{pre}.ff_context", oc.layer_norm(c, eps) * (1.0 + cc[4]) + cc[3])
+        return h, c
+    return fn
+
+
+def test_joint_block_variant_without_mistake_passes(monkeypatch):
+    """The planted variants below differ from the oracle only by their mistake."""
+    monkeypatch.setattr(osd, "joint_block", _joint_block_variant())
+    test_sd35_dual_block_one_image_one_text_token()
+    test_sd35_last_block_one_image_one_text_token()
+    test_sd35_joint_block_one_image_one_text_token_uniform()
+
+
+@pytest.mark.parametrize("mistake,test", [
+    (dict(dual_gate_chunk=2), "dual"), (dict(dual_gate_chunk=5), "dual"),
+    (dict(normed2_from_pre=False), "dual"), (dict(dual_before_ffn=False), "dual"),
+    (dict(last_text="zero_order"), "last"), (dict(last_text="plain"), "last")],
+    ids=["dual_gate_is_gate_msa", "dual_gate_from_chunk5", "normed2_after_attention", "dual_after_ffn",
+         "last_block_adaln_zero_order", "last_block_text_unmodulated"])
+def test_planted_joint_block_mistakes_are_caught(monkeypatch, mistake, test):
+    monkeypatch.setattr(osd, "joint_block", _joint_block_variant(**mistake))
+    check = test_sd35_dual_block_one_image_one_text_token if test == "dual" else test_sd35_last_block_one_image_one_text_token
+    with pytest.raises(AssertionError):
+        check()
+
+
 def test_sd35_forward_without_blocks_is_patch_embed_then_output():
     """forward() with no blocks = PatchEmbed (a library Conv2d plus the pinned table
     crop), AdaLayerNormContinuous (scale first, sd35_batch.py:379-393), proj_out and the

@@ -160,6 +160,20 @@ def test_condition_embedder_matches_module_composition():
         ref = te(oc.timestep_embedding(t, 256).double())
     assert torch.allclose(temb, ref, atol=1e-10)
     assert proj.shape == (1, 6, 256) and enc.shape == (6, 256)
+    # projected = time_proj(SiLU(temb)) unflattened as 6 chunks of D (transformer_wan.py:334-338;
+    # block.py:276-280 then reads chunk j as the j-th modulation vector)
+    tp = torch.nn.Sequential(torch.nn.SiLU(), torch.nn.Linear(256, 6 * 256)).double()
+    tp[1].weight.data, tp[1].bias.data = p[f"{pre}.time_proj.weight"], p[f"{pre}.time_proj.bias"]
+    with torch.no_grad():
+        flat = tp(ref)[0]
+    for j in range(6):
+        assert torch.allclose(proj[0, j], flat[j * 256:(j + 1) * 256], atol=1e-10)
+    # closed form: zero time_proj weight leaves the bias, chunk j = bias[j*D:(j+1)*D]
+    q = dict(p)
+    q[f"{pre}.time_proj.weight"] = torch.zeros_like(p[f"{pre}.time_proj.weight"])
+    q[f"{pre}.time_proj.bias"] = torch.arange(6 * 256, dtype=D64)
+    _, proj0, _ = ow.condition_embedder(q, t, text)
+    assert torch.equal(proj0[0], torch.arange(6 * 256, dtype=D64).reshape(6, 256))
     tx = torch.nn.Sequential(torch.nn.Linear(64, 256), torch.nn.GELU(approximate="tanh"), torch.nn.Linear(256, 256)).double()
     tx[0].weight.data, tx[0].bias.data = p[f"{pre}.text_embedder.linear_1.weight"], p[f"{pre}.text_embedder.linear_1.bias"]
     tx[2].weight.data, tx[2].bias.data = p[f"{pre}.text_embedder.linear_2.weight"], p[f"{pre}.text_embedder.linear_2.bias"]
@@ -279,6 +293,39 @@ def test_planted_dropped_gate_is_caught(monkeypatch):
     monkeypatch.setattr(ow, "split_modulation", wrong)
     with pytest.raises(AssertionError):
         test_wan_block_residual_structure()
+
+
+def _condition_embedder_variant(silu_before_proj=True, chunk_major=True):
+    """The oracle's condition embedder with one of two plausible mistakes: no SiLU
+    before time_proj, or the projection unflattened as (D, 6) instead of (6, D)."""
+    def fn(p, t, text, freq_dim=256):
+        pre = "condition_embedder"
+        e = oc.timestep_embedding(t, freq_dim).to(text.dtype)
+        temb = oc.linear(oc.silu(oc.linear(e, p[f"{pre}.time_embedder.linear_1.weight"],
+                                           p[f"{pre}.time_embedder.linear_1.bias"])),
+                         p[f"{pre}.time_embedder.linear_2.weight"], p[f"{pre}.time_embedder.linear_2.bias"])
+        x = oc.silu(temb) if silu_before_proj else temb
+        proj = oc.linear(x, p[f"{pre}.time_proj.weight"], p[f"{pre}.time_proj.bias"])
+        proj = proj.unflatten(-1, (6, -1)) if chunk_major else proj.unflatten(-1, (-1, 6)).transpose(-1, -2)
+        enc = oc.linear(oc.gelu_tanh(oc.linear(text, p[f"{pre}.text_embedder.linear_1.weight"],
+                                               p[f"{pre}.text_embedder.linear_1.bias"])),
+                        p[f"{pre}.text_embedder.linear_2.weight"], p[f"{pre}.text_embedder.linear_2.bias"])
+        return temb, proj, enc
+    return fn
+
+
+def test_condition_embedder_variant_without_mistake_passes(monkeypatch):
+    """The planted variants below differ from the oracle only by their mistake."""
+    monkeypatch.setattr(ow, "condition_embedder", _condition_embedder_variant())
+    test_condition_embedder_matches_module_composition()
+
+
+@pytest.mark.parametrize("mistake", [dict(silu_before_proj=False), dict(chunk_major=False)],
+                         ids=["no_silu_before_time_proj", "unflatten_d_by_6"])
+def test_planted_condition_embedder_mistakes_are_caught(monkeypatch, mistake):
+    monkeypatch.setattr(ow, "condition_embedder", _condition_embedder_variant(**mistake))
+    with pytest.raises(AssertionError):
+        test_condition_embedder_matches_module_composition()
 
 
 def test_planted_adaln_continuous_order_error_is_caught(monkeypatch):

@@ -25,6 +25,7 @@ Block arithmetic follows workers/ditserve/models/wan/block.py:276-297:
 """
 import dataclasses
 import math
+import weakref
 
 import torch
 
@@ -320,9 +321,10 @@ class WanTransformer:
         self.resolve_packet(packet)
         seg, seg_txt = packet["cu_seqlens_q"], packet["cu_seqlens_kv_text"]
         h = packet["hidden"]
-        with prof.region("modulation+adaln"):
+        with prof.region("modulation"):
             mod = ops.modulation(blk["sst"], packet["projected"])  # [R, 6, D] fp32
-            # self-attention (_stage1, block.py:282-285)
+        # self-attention (_stage1, block.py:282-285)
+        with prof.region("adaln"):
             x = ops.adaln(h, mod[:, 0], mod[:, 1], seg, eps=cfg.eps)
         with prof.region("gemm_qkv"):
             qkv = ops.linear(x, blk["qkv_w"], blk["qkv_b"])
@@ -338,7 +340,8 @@ class WanTransformer:
         # cross-attention (_stage2, block.py:288-290)
         with prof.region("cross_prep"):
             x = ops.adaln(h, weight=blk["n2_w"], bias=blk["n2_b"], eps=cfg.eps)
-            q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
+            with prof.region("gemm_cross_q"):
+                q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
             kv2 = ops.linear(packet["encoder"], blk["kv2_w"], blk["kv2_b"])
             k2, v2 = kv2[:, :D], kv2[:, D:]
             ops.adaln(q2, weight=blk["nq2_pre"], eps=cfg.eps, kind="rms", out=q2)
@@ -349,7 +352,7 @@ class WanTransformer:
         with prof.region("gemm_o_res"):
             ops.linear(a, blk["o2_w"], blk["o2_b"], "res", residual=h, out=h)
         # FFN (block.py:291-293)
-        with prof.region("modulation+adaln"):
+        with prof.region("adaln"):
             x = ops.adaln(h, mod[:, 3], mod[:, 4], seg, eps=cfg.eps)
         with prof.region("gemm_ffn_up_gelu"):
             f = ops.linear(x, blk["f1_w"], blk["f1_b"], "gelu")
@@ -391,7 +394,34 @@ class WanTransformer:
         return self.prediction_packed(packet)
 
 
-_SLOT_ROPE = {}
+_SLOT_ROPE = []  # [(weakref cos, weakref sin, cos version, sin version, (device, B, S, dh), Rope)]
+_SLOT_ROPE_MAX = 8
+
+
+def _slot_rope(freqs_cos, freqs_sin, device, B, S, dh):
+    """Rotation and segment tables of the slot for these exact table tensors.
+
+    An entry is reused only while the very tensors it was built from are alive and
+    unmodified: it holds weak references to them and their version counters, so a
+    new table that the caching allocator places at a freed table's address (the
+    reference builds fresh tables in every begin_packet, transformer_wan.py:326)
+    never matches an old entry."""
+    shape = (device, B, S, dh)
+    # entries whose tables were freed can never match again: drop them
+    _SLOT_ROPE[:] = [e for e in _SLOT_ROPE if e[0]() is not None and e[1]() is not None]
+    for e in _SLOT_ROPE:
+        if (e[0]() is freqs_cos and e[1]() is freqs_sin and e[2] == freqs_cos._version
+                and e[3] == freqs_sin._version and e[4] == shape):
+            return e[5]
+    # per-token tables: pair i uses cos[..., 2i] / sin[..., 2i+1]
+    cos_tab = freqs_cos.reshape(S, dh)[:, 0::2].float().contiguous()
+    sin_tab = freqs_sin.reshape(S, dh)[:, 1::2].float().contiguous()
+    seg = Segments([b * S for b in range(B + 1)], device)
+    rope = ops.Rope(cos_tab, sin_tab, [(S, 1, 1)] * B, seg, dh // 2, 0)
+    _SLOT_ROPE.append((weakref.ref(freqs_cos), weakref.ref(freqs_sin), freqs_cos._version, freqs_sin._version,
+                       shape, rope))
+    del _SLOT_ROPE[:-_SLOT_ROPE_MAX]
+    return rope
 
 
 def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
@@ -403,25 +433,14 @@ def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
 
     One out-of-place kernel launch covers the B requests (each a segment of S
     tokens whose position is its index on a single axis) and writes the new
-    tensors directly; the rotation tables and segment table built from
-    freqs_cos/sin are kept for the next call with the same tables, so a steady
-    call allocates only the two outputs."""
+    tensors directly.  The rotation and segment tables built from freqs_cos/sin
+    are kept while those same table tensors live unmodified (the 30 blocks of one
+    packet pass the same tables), so a steady call allocates only the two outputs."""
     B, S, D = query.shape
     dh = D // heads
     wq = getattr(norm_q, "weight", norm_q).float().contiguous()
     wk = getattr(norm_k, "weight", norm_k).float().contiguous()
-    key_ = (query.device, B, S, dh, freqs_cos.data_ptr(), freqs_cos._version, freqs_sin.data_ptr(),
-            freqs_sin._version)
-    rope = _SLOT_ROPE.get(key_)
-    if rope is None:
-        # per-token tables: pair i uses cos[..., 2i] / sin[..., 2i+1]
-        cos_tab = freqs_cos.reshape(S, dh)[:, 0::2].float().contiguous()
-        sin_tab = freqs_sin.reshape(S, dh)[:, 1::2].float().contiguous()
-        seg = Segments([b * S for b in range(B + 1)], query.device)
-        rope = ops.Rope(cos_tab, sin_tab, [(S, 1, 1)] * B, seg, dh // 2, 0)
-        if len(_SLOT_ROPE) >= 8:
-            _SLOT_ROPE.clear()
-        _SLOT_ROPE[key_] = rope
+    rope = _slot_rope(freqs_cos, freqs_sin, query.device, B, S, dh)
     qi, ki = query.reshape(B * S, D), key.reshape(B * S, D)
     if qi.dtype != _BF16 or qi.stride(1) != 1:
         qi = qi.to(_BF16).contiguous()

@@ -151,3 +151,27 @@ def test_fused_qk_norm_rope_slot():
     oq2, okk2 = wan.fused_qk_norm_rope(qd, kd, *args)
     assert torch.equal(oq2, oq) and torch.equal(okk2, okk)
     assert torch.equal(qd.cpu(), q.to(torch.bfloat16)) and torch.equal(kd.cpu(), k.to(torch.bfloat16))
+
+
+def test_fused_qk_norm_rope_slot_fresh_tables_of_equal_length():
+    """Two packets of equal S but different grids, (2, 6, 25) then (2, 10, 15): the
+    first packet's tables are freed before the second packet builds its own (as the
+    reference does per begin_packet, transformer_wan.py:326), so the caching
+    allocator may place them at the same address.  Each call must rotate with its
+    own tables."""
+    wan = _wan()
+    B, S, D, H = 1, 300, 1536, 12
+    q, k = bf(randn((B, S, D), 34)), bf(randn((B, S, D), 35))
+    wq, wk = bf(randn((D,), 36, 0.1) + 1), bf(randn((D,), 37, 0.1) + 1)
+    qd, kd = q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16)
+    ptrs = []
+    for grid in ((2, 6, 25), (2, 10, 15)):
+        cos, sin = ow.rope_freqs(grid)
+        cd, sd = cos.reshape(1, S, 1, 128).to(DEV), sin.reshape(1, S, 1, 128).to(DEV)
+        ptrs.append(cd.data_ptr())
+        oq, okk = wan.fused_qk_norm_rope(qd, kd, wq.to(DEV), wk.to(DEV), cd, sd, H)
+        rq, rk = ow.qk_norm_rope(q[0], k[0], wq, wk, cos, sin, H)
+        assert_close(oq[0].float().cpu(), rq, 0.99999, 5e-3, f"slot q {grid}")
+        assert_close(okk[0].float().cpu(), rk, 0.99999, 5e-3, f"slot k {grid}")
+        del cd, sd, oq, okk
+    print("table addresses", [hex(p) for p in ptrs], "reused" if ptrs[0] == ptrs[1] else "distinct")

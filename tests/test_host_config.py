@@ -40,3 +40,51 @@ def test_sd35_config_from_diffusers():
     assert SD35Config.from_diffusers(SD35M) == SD35_MEDIUM
     with pytest.raises(ValueError):
         SD35Config.from_diffusers(dict(SD35M, qk_norm=None))
+
+
+def test_slot_rope_cache_is_keyed_on_the_table_tensors(monkeypatch):
+    """The fused_qk_norm_rope slot reuses its rotation tables only for the very table
+    tensors it built them from, alive and unmodified.  A fresh table of the same shape
+    (the reference builds new ones per packet, transformer_wan.py:326), even when the
+    allocator hands it a freed table's storage, gets tables of its own."""
+    import torch
+
+    from ditserve_amd import wan
+
+    built = []
+
+    class FakeRope:
+        def __init__(self, cos_tab, sin_tab, *a):
+            self.cos = cos_tab
+            built.append(self)
+    monkeypatch.setattr(wan.ops, "Rope", FakeRope)
+    monkeypatch.setattr(wan, "Segments", lambda cu, device: None)
+    monkeypatch.setattr(wan, "_SLOT_ROPE", [])
+    S, dh = 6, 8
+    storage = torch.arange(S * dh, dtype=torch.float32)
+    c1, s1 = storage.view(1, S, 1, dh), torch.zeros(1, S, 1, dh)
+    r1 = wan._slot_rope(c1, s1, "cpu", 1, S, dh)
+    assert wan._slot_rope(c1, s1, "cpu", 1, S, dh) is r1           # same live tables: cached
+    del c1
+    c2 = storage.view(1, S, 1, dh)                                  # same address, new tensor
+    r2 = wan._slot_rope(c2, s1, "cpu", 1, S, dh)
+    assert r2 is not r1 and len(built) == 2
+    c2.mul_(2.0)                                                    # modified in place: rebuilt
+    r3 = wan._slot_rope(c2, s1, "cpu", 1, S, dh)
+    assert r3 is not r2 and torch.equal(r3.cos, c2.reshape(S, dh)[:, 0::2])
+    assert wan._slot_rope(c2, s1, "cpu", 2, S, dh) is not r3        # other batch size: rebuilt
+
+
+def test_view_extent_and_overlap():
+    """linear_pair's aliasing check: byte ranges of strided views."""
+    import torch
+
+    from ditserve_amd import ops
+    base = torch.zeros(10, 8, dtype=torch.bfloat16)
+    a, b = base[:4], base[4:]
+    assert ops._extent(a) == (a.data_ptr(), a.data_ptr() + 4 * 8 * 2)
+    assert not ops._overlap(a, b) and ops._overlap(base, b) and ops._overlap(a, base[3:5])
+    cols = base[:, 2:4]                                  # strided column slice: rows 0..9
+    assert ops._extent(cols) == (cols.data_ptr(), cols.data_ptr() + (9 * 8 + 2) * 2)
+    assert ops._overlap(cols, base[9:]) and not ops._overlap(base[:, :2][:1], base[:, 2:4][:1])
+    assert ops._extent(base[:0]) == (0, 0) and not ops._overlap(base[:0], base)

@@ -46,6 +46,7 @@ SIGNATURES = {
     "ditk_cfg_combine": (c_int, [_P, _P, _P, c_int64, c_float, _P]),
     "ditk_joint_copy": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "ditk_silu": (c_int, [_P, _P, c_int64, _P]),
+    "ditk_check_cu_seqlens": (c_int, [_P, c_int, c_int, _P, _P, _P]),
     "ditk_solver_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P]),
     "ditk_flash_attn_varlen_noalloc": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64,
                                                _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P]),

@@ -12,6 +12,12 @@ varlen flash kernel (bf16, head_dim 64/128, non-causal, no dropout).
    :448-486): ``flash_attn_varlen_func(q, k, v, cu_q, cu_k, max_q, max_k,
    dropout_p=0.0, causal=False) -> out`` on packed [T, H, D] tensors with int32
    device cu_seqlens.  No host synchronisation: cu tables stay on the device.
+
+Device cu_seqlens tables from callers are checked on the GPU before any kernel
+reads them (ops.Segments.from_device): an invalid table is clamped into bounds
+and reported by the next call after the check has finished, or by
+``check_tables()``.  BHSD calls without key packing reuse cached per-shape
+segment tables, so a steady call uploads nothing.
 """
 import dataclasses
 from typing import Optional
@@ -88,8 +94,8 @@ def ditk_attention(query, key, value, call=None):
             raise ValueError(f"varlen packing describes {seg_k.nseg} batches, query has {b}")
     else:
         k, v = _rows(key), _rows(value)
-        seg_k = ops.Segments([i * sk for i in range(b + 1)], query.device)
-    seg_q = ops.Segments([i * sq for i in range(b + 1)], query.device)
+        seg_k = ops.Segments.uniform(b, sk, query.device)
+    seg_q = ops.Segments.uniform(b, sq, query.device)
     out, lse = ops.flash_attn_varlen(q, k, v, seg_q, seg_k, h, d, return_lse=True)
     out = out.view(b, sq, h, d).transpose(1, 2)
     lse = lse.view(h, b, sq).permute(1, 0, 2)
@@ -113,3 +119,9 @@ def flash_attn_varlen_func(q, k, v, cu_q, cu_k, max_q, max_k, dropout_p=0.0, cau
     out = ops.flash_attn_varlen(q.reshape(tq, h * d), k.reshape(k.shape[0], h * d),
                                 v.reshape(v.shape[0], h * d).contiguous(), seg_q, seg_k, h, d)
     return out.view(tq, h, d)
+
+
+def check_tables(device=None):
+    """Wait for the device and raise if a cu_seqlens table passed to these entry
+    points since the last report was invalid (see ops.Segments.from_device)."""
+    ops.check_tables(device)

@@ -137,7 +137,52 @@ inline unsigned grid_for(int64_t n) {
   return (unsigned)(b > 65536 ? 65536 : (b < 1 ? 1 : b));
 }
 
+// A caller's device cu_seqlens table made safe for the segment kernels: out[0] = 0
+// and out[i] = max over j <= i of clamp(cu[j], 0, total), so the table is
+// nondecreasing inside [0, total] and every row a kernel derives from it exists.
+// A valid table (cu[0] = 0, nondecreasing, cu[n-1] = total) comes out unchanged;
+// any other sets bit 0 of *status (sticky: this kernel never clears it).  One
+// workgroup; chunks of 256 entries, each a block-wide running max on LDS.
+__global__ __launch_bounds__(256) void check_cu_kernel(const int32_t* __restrict__ cu, int n, int total,
+                                                       int32_t* __restrict__ out, int32_t* __restrict__ status) {
+  __shared__ int32_t sm[256];
+  const int tid = threadIdx.x;
+  int carry = 0, bad = 0;
+  for (int base = 0; base < n; base += 256) {
+    const int i = base + tid;
+    int v = 0;
+    if (i < n) {
+      const int raw = cu[i];
+      const int prev = i > 0 ? cu[i - 1] : 0;
+      bad |= (raw < prev) | (raw > total) | (i == 0 && raw != 0) | (i == n - 1 && raw != total);
+      v = min(max(raw, 0), total);
+    }
+    sm[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int x = tid >= off ? sm[tid - off] : 0;
+      __syncthreads();
+      sm[tid] = max(sm[tid], x);
+      __syncthreads();
+    }
+    if (i < n) out[i] = i == 0 ? 0 : max(sm[tid], carry);
+    carry = max(carry, sm[255]);
+    __syncthreads();
+  }
+  if (__syncthreads_or(bad) && tid == 0) atomicOr(status, 1);
+}
+
 }  // namespace
+
+DITK_EXPORT int ditk_check_cu_seqlens(const int32_t* cu, int nseg, int total, int32_t* cu_out, int32_t* status,
+                                      hipStream_t stream) {
+  DITK_REQUIRE(cu && cu_out && status, "ditk_check_cu_seqlens: null pointer");
+  DITK_REQUIRE(cu != cu_out, "ditk_check_cu_seqlens: cu_out must not be cu");
+  DITK_REQUIRE(nseg > 0 && nseg < (1 << 24) && total >= 0, "ditk_check_cu_seqlens: bad sizes (nseg %d, total %d)",
+               nseg, total);
+  check_cu_kernel<<<1, 256, 0, stream>>>(cu, nseg + 1, total, cu_out, status);
+  return ditk_check_launch("ditk_check_cu_seqlens");
+}
 
 DITK_EXPORT int ditk_patchify(const void* latent, void* out, int C, int F, int H, int W, int pt, int ph,
                               int pw, hipStream_t stream) {

@@ -74,16 +74,42 @@ class Segments:
 
     @classmethod
     def from_device(cls, cu_dev, total):
-        """Wrap a device int32 cu_seqlens tensor without reading it back (no host
-        sync).  The caller vouches that cu[0] = 0, cu is nondecreasing and
-        cu[-1] == total, as the reference's varlen callers do."""
+        """Wrap a caller's device int32 cu_seqlens tensor without reading it back
+        (no host sync).  A small kernel first copies it into a table of its own,
+        clamped so that every segment lies inside [0, total); a table that was not
+        valid (cu[0] != 0, a decrease, cu[-1] != total) sets the device's sticky
+        status, which the next call made after that kernel has finished raises
+        (table_status(...).poll()), or check_tables() raises after a sync."""
         if cu_dev.dtype != torch.int32 or cu_dev.dim() != 1 or cu_dev.numel() < 2 or cu_dev.device.type != "cuda":
             raise ValueError("cu_seqlens must be a 1-D int32 cuda tensor with at least 2 entries")
+        status = table_status(cu_dev.device)
+        status.poll()
         obj = cls.__new__(cls)
         obj.cu = None
-        obj.dev = cu_dev.contiguous()
+        obj.dev = torch.empty_like(cu_dev, memory_format=torch.contiguous_format)
         obj._nseg, obj._total = cu_dev.numel() - 1, int(total)
+        _lib.call("ditk_check_cu_seqlens", _ptr(cu_dev.contiguous()), obj._nseg, obj._total, _ptr(obj.dev),
+                  _ptr(status.dev), _stream())
+        status.queue_read()
         return obj
+
+    @classmethod
+    def uniform(cls, count, length, device):
+        """[0, length, 2 length, ...] for `count` equal segments, cached per
+        (device, count, length): after the first call no host upload happens.
+        The cached table is uploaded synchronously once, so any stream may read it."""
+        key = (torch.device(device), int(count), int(length))
+        seg = _UNIFORM.get(key)
+        if seg is None:
+            obj = cls.__new__(cls)
+            obj.cu = [i * int(length) for i in range(int(count) + 1)]
+            obj.dev = torch.tensor(obj.cu, dtype=torch.int32).to(device)
+            torch.cuda.current_stream(obj.dev.device).synchronize()
+            obj._nseg, obj._total = int(count), obj.cu[-1]
+            if len(_UNIFORM) >= 64:
+                _UNIFORM.clear()
+            seg = _UNIFORM[key] = obj
+        return seg
 
     @property
     def nseg(self):
@@ -107,6 +133,63 @@ class Segments:
         """Mark the device table as in use by ``stream`` (for packets consumed on a
         side stream, as the reference's interleaved executor does)."""
         self.dev.record_stream(stream)
+
+
+_UNIFORM = {}
+
+
+class TableStatus:
+    """Sticky per-device flag of ditk_check_cu_seqlens.  After each check a copy of
+    the flag goes to pinned host memory without blocking; poll() looks at it only
+    once that copy has completed (an event query, never a wait) and raises if a
+    table was invalid.  check() waits for the device and raises likewise."""
+
+    def __init__(self, device):
+        self.dev = torch.zeros(1, dtype=torch.int32, device=device)
+        self.host = torch.zeros(1, dtype=torch.int32).pin_memory()
+        self.event = None
+
+    def queue_read(self):
+        self.host.copy_(self.dev, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def _raise_if_set(self):
+        if int(self.host[0]) != 0:
+            self.host.zero_()
+            self.dev.zero_()
+            self.event = None
+            raise _lib.DitkError("an invalid cu_seqlens table reached the attention kernels (cu[0] != 0, "
+                                 "decreasing, or its last entry != the packed token count); it was clamped "
+                                 "into bounds, so those outputs are not attention over the intended segments")
+
+    def poll(self):
+        if self.event is not None and self.event.query():
+            self._raise_if_set()
+
+    def check(self):
+        torch.cuda.synchronize(self.dev.device)
+        self.host.copy_(self.dev)
+        self._raise_if_set()
+
+
+_STATUS = {}
+
+
+def table_status(device):
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    st = _STATUS.get(device)
+    if st is None:
+        st = _STATUS[device] = TableStatus(device)
+    return st
+
+
+def check_tables(device=None):
+    """Wait for `device` (default: the current one) and raise DitkError if a
+    caller's cu_seqlens table checked since the last report was invalid."""
+    table_status(device if device is not None else torch.device("cuda")).check()
 
 
 # ---------------------------------------------------------------------------
@@ -296,12 +379,27 @@ def linear(x, w, b=None, epilogue="bias", residual=None, gate=None, segments=Non
     return out
 
 
+def _extent(t):
+    """[first, last) byte range a strided view touches (0-size views touch nothing)."""
+    if t.numel() == 0:
+        return 0, 0
+    span = 1 + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+    return t.data_ptr(), t.data_ptr() + span * t.element_size()
+
+
+def _overlap(a, b):
+    a0, a1 = _extent(a)
+    b0, b1 = _extent(b)
+    return a0 < b1 and b0 < a1
+
+
 def linear_pair(p0, p1, epilogue="bias"):
     """Two linear() products of the same N, K and epilogue (e.g. an SD3.5 block's
     image and text projections), in one launch when their tiles fit the larger
     one's rounds.  p0, p1: dicts of linear()'s arguments (x, w, and optionally b,
     residual, gate, segments, out).  Returns (out0, out1), each bitwise what
-    linear() returns for it."""
+    linear() returns for it.  Each output may alias its own residual, but neither
+    output may overlap any operand or the output of the other product."""
     def args(p):
         return _linear_args(p["x"], p["w"], p.get("b"), epilogue, p.get("residual"), p.get("gate"),
                             p.get("segments"), p.get("out"))
@@ -309,6 +407,13 @@ def linear_pair(p0, p1, epilogue="bias"):
     o1, a1, N1, K1 = args(p1)
     if (N0, K0) != (N1, K1):
         raise ValueError(f"linear_pair needs one N and K (got {N0}x{K0} and {N1}x{K1})")
+    # the two products' tiles run concurrently in one launch or in order in two,
+    # whichever pays: one product's output may not overlap the other's operands
+    for out, other, name in ((o0, p1, "second"), (o1, p0, "first")):
+        for key in ("x", "w", "b", "residual", "gate", "out"):
+            t = other.get(key) if key != "out" else (o1 if out is o0 else o0)
+            if t is not None and _overlap(out, t):
+                raise ValueError(f"linear_pair: an output overlaps the {name} product's {key}")
     _lib.call("ditk_gemm_pair", *a0, *a1, N0, K0, EPILOGUES[epilogue], _stream())
     return o0, o1
 

@@ -97,7 +97,9 @@ int ditk_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const floa
  * operands (suffix 0 and 1; arguments as ditk_gemm's), in one launch when the
  * two tile lists together take no more rounds of the GPU's CUs than the larger
  * product alone, give or take 0.4 of a round (else two launches).  Every row
- * equals, bitwise, what ditk_gemm computes for it.
+ * equals, bitwise, what ditk_gemm computes for it.  Since the products may run
+ * concurrently, C0 must not overlap A1, W1, R1, bias1, gate1 or C1, nor C1 any
+ * of product 0's operands; each C may still alias its own R.
  * Replaces: the image- and context-stream projections of one SD3.5 joint block,
  *   issued back to back: attn.to_out / attn.to_add_out (sd35_batch.py:573-579)
  *   and the second linear of ff / ff_context (sd35_batch.py:698,707).
@@ -215,6 +217,20 @@ int ditk_joint_copy(void* img, int64_t ld_img, void* txt, int64_t ld_txt, void* 
 
 /* y = silu(x), bf16.  Replaces: the SiLU before time_proj / AdaLN linears. */
 int ditk_silu(const void* x, void* y, int64_t n, ditk_stream_t stream);
+
+/*
+ * A device cu_seqlens table handed in by a caller (int32 [nseg + 1]) checked on
+ * the GPU and made safe before a segment kernel reads it: cu_out[0] = 0 and
+ * cu_out[i] = the running max of cu[0..i] clamped into [0, total], so every row
+ * the kernels derive from cu_out exists.  A valid table (cu[0] = 0,
+ * nondecreasing, cu[nseg] = total) is copied unchanged; any other sets bit 0 of
+ * *status, which the kernel never clears (the host reads it after a later sync).
+ * No host synchronisation; cu_out must not be cu.
+ * Replaces: the trust the reference's varlen slot places in its device tables
+ *   (sd35_batch.py:448-486 passes cu_seqlens straight to the flash kernel).
+ */
+int ditk_check_cu_seqlens(const int32_t* cu, int nseg, int total, int32_t* cu_out, int32_t* status,
+                          ditk_stream_t stream);
 
 /*
  * Fused CFG combine + solver step for one request's fp32 latent of n elements,

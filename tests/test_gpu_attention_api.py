@@ -80,3 +80,68 @@ def test_sd35_varlen_slot(cu, d):
         api.flash_attn_varlen_func(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), v.to(DEV, torch.bfloat16),
                                    cu_t, cu_t, mx, mx, causal=True)
     _ = math
+
+
+@pytest.mark.parametrize("bad,clamped", [([0, 200, 400], [0, 200, 300]),      # past the token count
+                                         ([0, 250, 100, 300], [0, 250, 250, 300]),  # decreasing
+                                         ([5, 100, 300], [0, 100, 300]),       # not starting at 0
+                                         ([0, 100, 299], [0, 100, 299])])      # short of the token count
+def test_sd35_varlen_slot_invalid_tables_are_clamped_and_reported(bad, clamped):
+    """A caller's device cu table that is not valid is copied, clamped into [0, T]
+    and made nondecreasing, on the GPU before any kernel reads it, so no kernel
+    leaves the tensors; the sticky status reports it: check_tables() after a sync,
+    and the next call once the check has finished.  Valid calls then run as before."""
+    api = _api()
+    from ditserve_amd import ops
+    from ditserve_amd._lib import DitkError
+    h, d, t = 2, 64, 300
+    q, k, v = bf(randn((t, h, d), 10)), bf(randn((t, h, d), 11)), bf(randn((t, h, d), 12))
+    qd, kd, vd = (x.to(DEV, torch.bfloat16) for x in (q, k, v))
+    good = torch.tensor([0, 120, 300], dtype=torch.int32, device=DEV)
+    badt = torch.tensor(bad, dtype=torch.int32, device=DEV)
+    api.flash_attn_varlen_func(qd, kd, vd, good, good, 180, 180)
+    api.check_tables()                                   # nothing to report
+    seg = ops.Segments.from_device(badt, t)
+    assert seg.dev.tolist() == clamped and badt.tolist() == bad
+    with pytest.raises(DitkError):
+        api.check_tables()
+    api.check_tables()                                   # reported once
+    with pytest.raises(DitkError):
+        # reported by the first table check that starts after the bad table's
+        # check has finished: the bad call's key table, or the next call
+        api.flash_attn_varlen_func(qd, kd, vd, badt, badt, 300, 300)
+        torch.cuda.synchronize()
+        api.flash_attn_varlen_func(qd, kd, vd, good, good, 180, 180)
+    out = api.flash_attn_varlen_func(qd, kd, vd, good, good, 180, 180)
+    api.check_tables()
+    assert_close(out.float().cpu(), oc.varlen_attention(q, k, v, [0, 120, 300], [0, 120, 300]), 0.9999, 1e-2,
+                 "after report")
+
+
+def test_cu_table_check_across_chunks():
+    """Tables longer than the check kernel's 256-entry chunk: a valid 600-segment
+    table is copied unchanged and not reported; a dip at entry 300 is clamped with
+    the running max carried over from the earlier chunks."""
+    from ditserve_amd import ops
+    from ditserve_amd._lib import DitkError
+    cu = [3 * i for i in range(601)]
+    seg = ops.Segments.from_device(torch.tensor(cu, dtype=torch.int32, device=DEV), cu[-1])
+    assert seg.dev.tolist() == cu
+    ops.check_tables()
+    dip = list(cu)
+    dip[300] = 5
+    seg = ops.Segments.from_device(torch.tensor(dip, dtype=torch.int32, device=DEV), cu[-1])
+    assert seg.dev.tolist() == cu[:300] + [cu[299]] + cu[301:]
+    with pytest.raises(DitkError):
+        ops.check_tables()
+
+
+def test_backend_uniform_tables_are_cached():
+    """ditk_attention without key packing reuses one device table per shape."""
+    api = _api()
+    from ditserve_amd import ops
+    x = torch.zeros((2, 2, 77, 64), dtype=torch.bfloat16, device=DEV)
+    api.ditk_attention(x, x, x)
+    a = ops.Segments.uniform(2, 77, DEV)
+    api.ditk_attention(x, x, x)
+    assert ops.Segments.uniform(2, 77, DEV) is a and a.dev.tolist() == [0, 77, 154]

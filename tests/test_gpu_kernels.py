@@ -176,7 +176,7 @@ def test_gemm_short_tile_row_split_agrees(epi):
     assert_close(y[rows].float(), ref, 0.999, 1e-2, f"split {epi}")
 
 
-@pytest.mark.parametrize("epi", ["gate_res", "bias", "gelu", "res"])
+@pytest.mark.parametrize("epi", ["gate_res", "bias", "gelu", "res", "silu"])
 @pytest.mark.parametrize("M0,M1,N,K", [(8192, 666, 1536, 1536),   # one launch: 192 + 18 tiles = one round
                                        (666, 8192, 1536, 6144),   # the same, text first, long K
                                        (8192, 666, 4608, 1536)])  # two launches: the text tiles add a round
@@ -202,6 +202,37 @@ def test_gemm_pair_matches_separate(epi, M0, M1, N, K):
     assert torch.equal(y1, ops.linear(epilogue=epi, **p1)), "second product"
     with pytest.raises(ValueError):
         ops.linear_pair(p0, dict(x=p1["x"][:, :K - 32].contiguous(), w=p1["w"][:, :K - 32].contiguous()), epi)
+
+
+@pytest.mark.parametrize("epi", ["gate_res", "res"])
+def test_gemm_pair_in_place_matches_separate(epi):
+    """SD3.5's block calls the pair in place (out = residual = h for the image rows,
+    out = residual = c for the text rows).  At (8192, 666, 1536, 1536) the pair runs
+    in one launch; each product's in-place result equals, bitwise, an in-place
+    ditk_gemm on a copy.  Overlap between the products is refused on the host."""
+    ops = _ops()
+    N = K = 1536
+
+    def prob(M, seed):
+        p = dict(x=randn((M, K), seed).to(DEV, torch.bfloat16), w=randn((N, K), seed + 1, 0.02).to(DEV, torch.bfloat16),
+                 b=randn((N,), seed + 2).to(DEV), residual=randn((M, N), seed + 3).to(DEV, torch.bfloat16))
+        if epi == "gate_res":
+            p["gate"] = randn((2, N), seed + 4).to(DEV)
+            p["segments"] = _seg([0, M // 2 + 7, M])
+        return p
+
+    p0, p1 = prob(8192, 90), prob(666, 95)
+    ref0 = p0["residual"].clone()
+    ref1 = p1["residual"].clone()
+    ops.linear(epilogue=epi, **dict(p0, residual=ref0, out=ref0))
+    ops.linear(epilogue=epi, **dict(p1, residual=ref1, out=ref1))
+    p0["out"], p1["out"] = p0["residual"], p1["residual"]
+    y0, y1 = ops.linear_pair(p0, p1, epi)
+    assert y0.data_ptr() == p0["residual"].data_ptr() and y1.data_ptr() == p1["residual"].data_ptr()
+    assert torch.equal(y0, ref0), "image rows in place"
+    assert torch.equal(y1, ref1), "text rows in place"
+    with pytest.raises(ValueError):   # product 1 reads rows product 0 writes
+        ops.linear_pair(p0, dict(p1, x=p0["residual"][:666]), epi)
 
 
 def test_gemm_stage_depths_agree():

@@ -1,5 +1,8 @@
 """Wan at full working-set sizes on the GPU.
 
+* Wan2.1-T2V-1.3B architecture, 30 blocks, latent 16x21x60x104 (480x832x81
+  frames): the CFG pair packed as 2 x 32760 tokens, each segment bitwise equal to
+  its solo forward.
 * Wan2.2-TI2V-5B architecture, 30 blocks, latent 48x31x44x80 (704x1280x121 frames):
   the CFG pair packed as 2 x 27280 tokens (text valid 150 / 0, t = 700) gives finite
   outputs, each segment bitwise equal to its solo forward.
@@ -36,6 +39,24 @@ def test_wan22_5b_30_blocks_full_latent_cfg_pair_bitwise():
         assert out.shape == (48, 31, 44, 80) and bool(torch.isfinite(out).all())
         solo = model.forward_packed([lat], [700.0], [txt])[0]
         assert torch.equal(out, solo)
+    assert not torch.equal(both[0], both[1])
+
+
+def test_wan21_30_blocks_480p_cfg_pair_bitwise():
+    """The headline workload's shape: Wan2.1-1.3B architecture, 30 blocks, latent
+    16x21x60x104 (480x832x81 frames), the CFG pair packed as 2 x 32760 tokens (text
+    valid 120 / 0, t = 999): each segment of the packed forward equals, bitwise,
+    the forward of that request alone."""
+    from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer
+    model = WanTransformer.random(WAN21_T2V_1_3B, seed=9, device=DEV)
+    lat = randn((16, 21, 60, 104), 52).to(DEV)
+    tc, tu = _text(53, 120).to(DEV), torch.zeros(512, 4096, device=DEV)
+    packet = model.begin_packed_packet([lat, lat], [999.0, 999.0], [tc, tu])
+    assert packet["cu_seqlens_q"].cu == [0, 32760, 65520]
+    both = model.forward_packed([lat, lat], [999.0, 999.0], [tc, tu])
+    for out, txt in zip(both, (tc, tu)):
+        assert out.shape == (16, 21, 60, 104) and bool(torch.isfinite(out).all())
+        assert torch.equal(out, model.forward_packed([lat], [999.0], [txt])[0])
     assert not torch.equal(both[0], both[1])
 
 

@@ -20,11 +20,17 @@ attention roofline fraction and CPU baseline:
                           U[0,1000) and texts (valid 30-200): one packed forward;
   * sd35_medium_1024_cfg2 SD3.5-Medium 1024^2 step, CFG pair of joint segments
                           (4096 image + 333 text tokens each), FlowMatch-Euler;
+  * sd35_packed_2x1024_4x512_cfg2  SD3.5-Medium packed step over 2 x 1024^2 +
+                          4 x 512^2 requests, each a CFG pair (12 joint segments),
+                          per-request FlowMatch-Euler;
   * wan22_ti2v_5b_704p_cfg2  Wan2.2-TI2V-5B 704x1280x121f step, CFG pair of
                           2 x 27280 tokens, text valid 150/0, t = 700 schedule.
 
 Prints one JSON line.  ``roofline`` is for the dominant kernel, the self-attention
 flash kernel, from HIP events recorded on its launch stream over the timed steps.
+``kernels`` (per config) gives every hot kernel's roofline -- GEMMs and attention
+as TFLOP/s of the 2.5 PFLOP/s bf16 peak, the row kernels as TB/s of 8 TB/s HBM --
+from HIP events around each kernel over one more step after the timed ones.
 ``cpu_baseline`` times the oracle (the CPU fp32 restatement of the reference block)
 on one full-shape block-forward and extrapolates to the step (blocks x branches).
 """
@@ -35,6 +41,7 @@ import sys
 import time
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_TBS = 8.0
 CALIB_BYTES = 256 << 20
 GUIDANCE = 5.0
 SCHEDULE_STEPS = 50
@@ -55,6 +62,10 @@ WORKLOADS = {
     "sd35_medium_1024": dict(
         metric="denoise steps/s & tokens/s, SD3.5-Medium 1024x1024 CFG2; joint attn % bf16 MFMA peak",
         latent=(16, 128, 128), text_len=333, steps=28, shift=3.0, ref_ms=217.23),
+    "sd35_packed_2x1024_4x512": dict(
+        metric="packed denoise steps/s & tokens/s, SD3.5-Medium 2x1024^2 + 4x512^2 requests, CFG2 each "
+               "(12 joint segments); joint attn % bf16 MFMA peak",
+        sizes=(1024, 1024, 512, 512, 512, 512), text_len=333, steps=28, shift=3.0, guidance=7.0),
     "wan21_packed_4req": dict(
         metric="packed forwards/s & tokens/s, Wan2.1-1.3B 4-request varlen batch (56400 tokens); "
                "attn % bf16 MFMA peak",
@@ -175,11 +186,9 @@ def cpu_baseline_wan_block(cfg, threads, repeats=5):
                        f"median of {repeats} after 2 warm-ups", **_cpu_info(threads))
 
 
-def cpu_baseline_sd35(cfg, n_img, text_len, threads):
-    """One dual-attention and one plain SD3.5 joint block on one CFG branch
-    (n_img image + text_len text tokens), extrapolated to the step:
-    2 branches x (dual x 13 + plain x 11) -- the last block, which drops its
-    text stream, is counted as plain."""
+def _cpu_sd35_block_s(cfg, n_img, text_len):
+    """Seconds of one dual-attention and one plain oracle SD3.5 joint block on one
+    segment (n_img image + text_len text tokens), fp32, torch's CPU flash SDPA."""
     import torch
 
     from ditserve_amd.sd35 import SD35Config, random_state_dict
@@ -199,14 +208,40 @@ def cpu_baseline_sd35(cfg, n_img, text_len, threads):
         t0 = time.perf_counter()
         osd.joint_block(sd, i, h, c, temb, ocfg, attn=oc.sdpa_fast)
         times[name] = time.perf_counter() - t0
+    return times["dual"], times["plain"]
+
+
+def cpu_baseline_sd35(cfg, n_img, text_len, threads):
+    """One dual-attention and one plain SD3.5 joint block on one CFG branch
+    (n_img image + text_len text tokens), extrapolated to the step:
+    2 branches x (dual x 13 + plain x 11) -- the last block, which drops its
+    text stream, is counted as plain."""
+    dual, plain = _cpu_sd35_block_s(cfg, n_img, text_len)
     n_dual = len(cfg.dual_layers)
-    step_s = 2 * (times["dual"] * n_dual + times["plain"] * (cfg.layers - n_dual))
-    return dict(value=1.0 / step_s, unit="steps/s", tokens_per_s=2 * n_img / step_s, dual_block_s=times["dual"],
-                plain_block_s=times["plain"],
+    step_s = 2 * (dual * n_dual + plain * (cfg.layers - n_dual))
+    return dict(value=1.0 / step_s, unit="steps/s", tokens_per_s=2 * n_img / step_s, dual_block_s=dual,
+                plain_block_s=plain,
                 sample=f"1 dual + 1 plain SD3.5-M joint block ({n_img} image + {text_len} text tokens, one CFG "
-                       f"branch), fp32, CPU flash SDPA, {threads} threads: {times['dual']:.2f} s + "
-                       f"{times['plain']:.2f} s; extrapolated x2 branches x ({n_dual} dual + "
+                       f"branch), fp32, CPU flash SDPA, {threads} threads: {dual:.2f} s + "
+                       f"{plain:.2f} s; extrapolated x2 branches x ({n_dual} dual + "
                        f"{cfg.layers - n_dual} plain blocks)", **_cpu_info(threads))
+
+
+def cpu_baseline_sd35_packed(cfg, sizes, text_len, threads):
+    """The packed batch's blocks are per-segment on the CPU: one dual and one plain
+    joint block per distinct request size (one CFG branch), extrapolated to the
+    step as sum over requests of 2 branches x (dual x 13 + plain x 11)."""
+    per = {size: _cpu_sd35_block_s(cfg, (size // 16) ** 2, text_len) for size in sorted(set(sizes))}
+    n_dual = len(cfg.dual_layers)
+    step_s = sum(2 * (per[s][0] * n_dual + per[s][1] * (cfg.layers - n_dual)) for s in sizes)
+    n_img = sum(2 * (s // 16) ** 2 for s in sizes)
+    parts = ", ".join(f"{s}^2 ({(s // 16) ** 2} image tokens): {per[s][0]:.2f} s + {per[s][1]:.2f} s"
+                      for s in sorted(per))
+    return dict(value=1.0 / step_s, unit="steps/s", tokens_per_s=n_img / step_s,
+                block_s={str(s): {"dual": per[s][0], "plain": per[s][1]} for s in per},
+                sample=f"1 dual + 1 plain SD3.5-M joint block per request size, one segment with {text_len} text "
+                       f"tokens, fp32, CPU flash SDPA, {threads} threads: {parts}; extrapolated over the 6 requests "
+                       f"x 2 branches x ({n_dual} dual + {cfg.layers - n_dual} plain blocks)", **_cpu_info(threads))
 
 
 # ---------------------------------------------------------------------------
@@ -225,8 +260,16 @@ def _roofline(kernel, flops_per_launch, region, traffic=None, algorithmic_bytes=
     return out
 
 
+KERNEL_STEPS = 1
+
+
 def _timed(step, state, steps, warmup, prof_model, only, breakdown):
-    """Run warmup + timed steps; returns (state, ms per step, region summary)."""
+    """Run warmup + timed steps; returns (state, ms per step, region summary of the
+    timed steps, region summary of every region over KERNEL_STEPS further steps).
+
+    The timed steps record events only around the `only` regions (each event pair
+    costs host time); the per-kernel table comes from the extra steps after the
+    timed region, with every region recorded, and does not enter ms per step."""
     import torch
 
     from ditserve_amd.profiling import EventProfiler
@@ -243,8 +286,72 @@ def _timed(step, state, steps, warmup, prof_model, only, breakdown):
         state = step(state)
     end.record()
     torch.cuda.synchronize()
+    kprof = EventProfiler(enabled=True)
+    prof_model.profiler = kprof
+    for _ in range(KERNEL_STEPS):
+        state = step(state)
+    torch.cuda.synchronize()
     prof_model.profiler = EventProfiler(enabled=False)
-    return state, start.elapsed_time(end) / steps, prof.summary()
+    return state, start.elapsed_time(end) / steps, prof.summary(), kprof.summary()
+
+
+def _kernel_table(regions, spec):
+    """{name: roofline entry} from HIP-event region averages.  spec: {region: (bound,
+    work per region occurrence, what the region holds)}; "mfma" work is FLOP, "hbm"
+    work is algorithmic bytes (minimal reads + writes)."""
+    out = {}
+    for name, (bound, work, what) in spec.items():
+        r = regions.get(name)
+        if not r:
+            continue
+        sec = r["avg_ms"] * 1e-3
+        if bound == "mfma":
+            ach, peak, unit = work / sec / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = work / sec / 1e12, PEAK_HBM_TBS, "TB/s"
+        out[name] = {"what": what, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
+                     "frac": ach / peak, "avg_launch_ms": r["avg_ms"], "launches": r["count"],
+                     ("flops_per_launch" if bound == "mfma" else "bytes_per_launch"): work}
+    return out
+
+
+def _wan_kernel_spec(cfg, seqs, text_len):
+    """Per-kernel work of one Wan block over the packed rows (M = all tokens)."""
+    M, D, F = sum(seqs), cfg.dim, cfg.ffn
+    return {
+        "attn_self": ("mfma", 4.0 * sum(s * s for s in seqs) * D, "self-attention flash kernel"),
+        "attn_cross": ("mfma", 4.0 * M * text_len * D, f"cross-attention over {text_len} text keys per segment"),
+        "gemm_qkv": ("mfma", 2.0 * M * 3 * D * D, f"fused QKV projection {M}x{3 * D}x{D}, bias"),
+        "gemm_o_gate": ("mfma", 2.0 * M * D * D, f"self-attention output projection {M}x{D}x{D}, gated residual"),
+        "gemm_cross_q": ("mfma", 2.0 * M * D * D, f"cross-attention q projection {M}x{D}x{D}, bias"),
+        "gemm_o_res": ("mfma", 2.0 * M * D * D, f"cross-attention output projection {M}x{D}x{D}, residual"),
+        "gemm_ffn_up_gelu": ("mfma", 2.0 * M * F * D, f"FFN up {M}x{F}x{D}, GELU-tanh"),
+        "gemm_ffn_down_gate": ("mfma", 2.0 * M * D * F, f"FFN down {M}x{D}x{F}, gated residual"),
+        "adaln": ("hbm", 4.0 * M * D, "AdaLN (LayerNorm + per-segment shift/scale), bf16 in + out"),
+        "qk_norm_rope": ("hbm", 8.0 * M * D, "QK RMSNorm across heads + 3D RoPE, in place on q and k"),
+        "transpose_v": ("hbm", 4.0 * M * D, "V -> per-head transposed Vt staging, bf16 in + out"),
+    }
+
+
+def _sd35_kernel_spec(cfg, img_counts, txt_counts):
+    """Per-kernel work of one SD3.5 joint block over the packed rows."""
+    D, F = cfg.dim, cfg.ffn
+    Mi, Mt = sum(img_counts), sum(txt_counts)
+    joint = sum((n + l) ** 2 for n, l in zip(img_counts, txt_counts))
+    return {
+        "attn_joint": ("mfma", 4.0 * joint * D, "joint image+text attention, head_dim 64"),
+        "attn_dual_core": ("mfma", 4.0 * sum(n * n for n in img_counts) * D, "dual image-only attention, head_dim 64"),
+        "gemm_qkv_img": ("mfma", 2.0 * Mi * 3 * D * D, f"image QKV {Mi}x{3 * D}x{D}, bias"),
+        "gemm_qkv_txt": ("mfma", 2.0 * Mt * 3 * D * D, f"text QKV {Mt}x{3 * D}x{D}, bias"),
+        "gemm_out_pair": ("mfma", 2.0 * (Mi + Mt) * D * D,
+                          f"image + text output projections ({Mi} + {Mt})x{D}x{D}, gated residual, one pair call"),
+        "gemm_ffn_up_img": ("mfma", 2.0 * Mi * F * D, f"image FFN up {Mi}x{F}x{D}, GELU-tanh"),
+        "gemm_ffn_down_pair": ("mfma", 2.0 * (Mi + Mt) * D * F,
+                               f"image + text FFN down ({Mi} + {Mt})x{D}x{F}, gated residual, one pair call"),
+        "adaln_img": ("hbm", 4.0 * Mi * D, "image AdaLN-Zero (LayerNorm + per-segment shift/scale)"),
+        "qk_norm_img": ("hbm", 8.0 * Mi * D, "image per-head QK RMSNorm, in place on q and k"),
+        "transpose_v_joint": ("hbm", 4.0 * (Mi + Mt) * D, "image + text V -> joint transposed Vt staging"),
+    }
 
 
 def _release():
@@ -279,14 +386,14 @@ def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
     grid = (latent_shape[1] // pt, latent_shape[2] // ph, latent_shape[3] // pw)
     seq = grid[0] * grid[1] * grid[2]
     sched = UniPCFlowScheduler(flow_shift=wl["flow_shift"])
-    sched.set_timesteps(max(SCHEDULE_STEPS, warmup + steps))
+    sched.set_timesteps(max(SCHEDULE_STEPS, warmup + steps + KERNEL_STEPS))
 
     def step(lat):
         t = float(sched.timesteps[sched.step_index])
         cond, uncond = model.forward_packed([lat, lat], [t, t], texts)
         return sched.step(cond, t, lat, uncond=uncond, guidance=GUIDANCE)[0]
 
-    latent, ms, regions = _timed(step, latent, steps, warmup, model, {"attn_self"}, breakdown)
+    latent, ms, regions, kregions = _timed(step, latent, steps, warmup, model, {"attn_self"}, breakdown)
     if not bool(torch.isfinite(latent).all()):
         raise RuntimeError(f"{name}: non-finite latent after the timed steps")
     if calibrate:
@@ -312,6 +419,7 @@ def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
                               attn_flops, regions["attn_self"],
                               ATTN_SELF_TRAFFIC_BYTES if name == "wan21_480p" else None,
                               4.0 * 2 * seq * cfg.dim * 2),
+        "kernels": _kernel_table(kregions, _wan_kernel_spec(cfg, [seq, seq], cfg.text_len)),
         "reference_a100_ms_per_step": wl["ref_ms"], "vs_reference_a100": wl["ref_ms"] / ms,
         "_grid": grid, "_cfg": cfg,
     }
@@ -345,7 +453,7 @@ def run_wan_packed(steps, warmup, breakdown=False):
     def step(_):
         return model.forward_packed(lats, ts, texts)
 
-    outs, ms, regions = _timed(step, None, steps, warmup, model, {"attn_self"}, breakdown)
+    outs, ms, regions, kregions = _timed(step, None, steps, warmup, model, {"attn_self"}, breakdown)
     if not all(bool(torch.isfinite(o).all()) for o in outs):
         raise RuntimeError("packed Wan forward produced non-finite values")
     attn_flops = 4.0 * sum(s * s for s in seqs) * cfg.dim
@@ -364,6 +472,7 @@ def run_wan_packed(steps, warmup, breakdown=False):
         "roofline": _roofline(f"flash_fwd_asm<128, true> (self-attention, 4 segments, {tokens} tokens x "
                               f"{cfg.heads} heads)", attn_flops, regions["attn_self"],
                               algorithmic_bytes=4.0 * tokens * cfg.dim * 2),
+        "kernels": _kernel_table(kregions, _wan_kernel_spec(cfg, seqs, cfg.text_len)),
         "reference_a100_ms_per_step": None, "vs_reference_a100": None,
         "_grids": grids,
     }
@@ -389,7 +498,7 @@ def run_sd35(steps, warmup, breakdown=False):
     pooled_c = torch.randn((cfg.pooled_dim,), generator=g, device=dev)
     text_u, pooled_u = torch.zeros_like(text_c), torch.zeros_like(pooled_c)
     sched = FlowMatchEulerScheduler(shift=wl["shift"])
-    sched.set_timesteps(max(wl["steps"], warmup + steps))
+    sched.set_timesteps(max(wl["steps"], warmup + steps + KERNEL_STEPS))
     n_img = (wl["latent"][1] // cfg.patch) * (wl["latent"][2] // cfg.patch)
     n_joint = n_img + wl["text_len"]
 
@@ -399,7 +508,7 @@ def run_sd35(steps, warmup, breakdown=False):
                                       [text_u.unsqueeze(0), text_c.unsqueeze(0)], [pooled_u, pooled_c])
         return sched.step(outs[1], t, lat, uncond=outs[0], guidance=7.0)[0]
 
-    latent, ms, regions = _timed(step, latent, steps, warmup, model, {"attn_joint"}, breakdown)
+    latent, ms, regions, kregions = _timed(step, latent, steps, warmup, model, {"attn_joint"}, breakdown)
     if not bool(torch.isfinite(latent).all()):
         raise RuntimeError("sd35: non-finite latent after the timed steps")
     attn_flops = 4.0 * 2 * n_joint * n_joint * cfg.dim
@@ -415,8 +524,80 @@ def run_sd35(steps, warmup, breakdown=False):
         "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "roofline": _roofline(f"flash_fwd_asm<64, true, true> (joint attention, 2 x {n_joint} tokens x {cfg.heads} heads)",
                               attn_flops, regions["attn_joint"], algorithmic_bytes=4.0 * 2 * n_joint * cfg.dim * 2),
+        "kernels": _kernel_table(kregions, _sd35_kernel_spec(cfg, [n_img, n_img], [wl["text_len"]] * 2)),
         "reference_a100_ms_per_step": wl["ref_ms"], "vs_reference_a100": wl["ref_ms"] / ms,
         "_n_img": n_img, "_cfg": cfg,
+    }
+    if breakdown:
+        out["breakdown_ms_per_step"] = {k: v["total_ms"] / steps for k, v in regions.items()}
+    return out
+
+
+def run_sd35_packed(steps, warmup, breakdown=False):
+    """SD3.5-Medium packed batch of 2 x 1024^2 + 4 x 512^2 requests, each a CFG pair
+    (unconditional then conditional segment, workers/ditserve/models/sd35.py:919-930):
+    12 joint segments in one packed forward per step, then each request's own
+    FlowMatch-Euler update on its CFG-combined output (step_members_once, the
+    reference's _step_members_once)."""
+    import torch
+
+    from ditserve_amd.packing import build_cu_seqlens
+    from ditserve_amd.sd35 import SD35_MEDIUM, SD35Transformer, step_flops, step_members_once
+    from ditserve_amd.solver import FlowMatchEulerScheduler
+
+    wl = WORKLOADS["sd35_packed_2x1024_4x512"]
+    cfg, dev = SD35_MEDIUM, "cuda"
+    model = SD35Transformer.random(cfg, seed=0, device=dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    n_steps = max(wl["steps"], warmup + steps + KERNEL_STEPS)
+    states = []
+    for size in wl["sizes"]:
+        lat = torch.randn((1, 16, size // 8, size // 8), generator=g, device=dev)
+        txt = torch.randn((1, wl["text_len"], cfg.text_dim), generator=g, device=dev)
+        pooled = torch.randn((1, cfg.pooled_dim), generator=g, device=dev)
+        sched = FlowMatchEulerScheduler(shift=wl["shift"])
+        sched.set_timesteps(n_steps)
+        emb = dict(prompt_embeds=txt, pooled_prompt_embeds=pooled, negative_prompt_embeds=torch.zeros_like(txt),
+                   negative_pooled_prompt_embeds=torch.zeros_like(pooled))
+        states.append(dict(latents=lat, timesteps=sched.timesteps, step=0, scheduler=sched, embeds=emb,
+                           spec=dict(height=size, width=size, guidance_scale=wl["guidance"], steps=n_steps)))
+    img = [(s // 16) ** 2 for s in wl["sizes"] for _ in range(2)]  # CFG: two segments per request
+    txt_counts = [wl["text_len"]] * len(img)
+    meta = {}
+
+    def step(_):
+        meta.update(step_members_once(model, states))
+        return None
+
+    _, ms, regions, kregions = _timed(step, None, steps, warmup, model, {"attn_joint"}, breakdown)
+    if not all(bool(torch.isfinite(st["latents"]).all()) for st in states):
+        raise RuntimeError("sd35 packed: non-finite latents after the timed steps")
+    if meta.get("cu_seqlens_img") != build_cu_seqlens(img):
+        raise RuntimeError(f"sd35 packed: unexpected segment table {meta.get('cu_seqlens_img')}")
+    joint = [n + l for n, l in zip(img, txt_counts)]
+    attn_flops = 4.0 * sum(j * j for j in joint) * cfg.dim
+    total_flops = step_flops(cfg, img, txt_counts)
+    n_img = sum(img)
+    out = {
+        "metric": wl["metric"], "value": 1000.0 / ms, "unit": "steps/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "tokens_per_s": n_img * 1000.0 / ms,
+        "workload": (f"SD3.5-Medium-architecture packed denoise step over 6 requests (2 x 1024^2 + 4 x 512^2), "
+                     f"each a CFG pair: 12 joint segments, {n_img} image + {sum(txt_counts)} text tokens, "
+                     f"cu_seqlens_img {build_cu_seqlens(img)}, {cfg.layers} blocks, per-request "
+                     f"FlowMatch-Euler shift {wl['shift']:g}"),
+        "tokens_per_step": sum(joint), "blocks": cfg.layers,
+        "model_tflops": total_flops / (ms * 1e-3) / 1e12,
+        "model_mfma_frac": total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "roofline": _roofline(f"flash_fwd_asm<64, true, true> (joint attention, 12 segments, {sum(joint)} tokens x "
+                              f"{cfg.heads} heads)", attn_flops, regions["attn_joint"],
+                              algorithmic_bytes=4.0 * sum(joint) * cfg.dim * 2),
+        "kernels": _kernel_table(kregions, _sd35_kernel_spec(cfg, img, txt_counts)),
+        "reference_a100_ms_per_step": None, "vs_reference_a100": None,
+        "reference_context": ("the reference publishes packed SD3.5-M steps of 260.09 ms (1 x 512^2 + 1 x 1024^2) "
+                              "and 1003.32 ms (4 x 512^2 + 4 x 1024^2) on one A100-PCIe, results/3.3_Characterization"
+                              "_III_Cross-Modal_HBM_Wall_Prompt_Padding_and_Batch_Waste/README.md:32,35; neither is "
+                              "this request set"),
+        "_img": img, "_cfg": cfg,
     }
     if breakdown:
         out["breakdown_ms_per_step"] = {k: v["total_ms"] / steps for k, v in regions.items()}
@@ -475,6 +656,8 @@ def main():
     def headline_for(name, steps, warmup, calibrate=False):
         if name == "sd35_medium_1024":
             return run_sd35(steps, warmup, args.breakdown)
+        if name == "sd35_packed_2x1024_4x512":
+            return run_sd35_packed(steps, warmup, args.breakdown)
         if name == "wan21_packed_4req":
             return run_wan_packed(steps, warmup, args.breakdown)
         return run_wan_cfg(name, steps, warmup, args.breakdown, calibrate)
@@ -483,6 +666,9 @@ def main():
         torch.set_num_threads(threads)
         if name == "sd35_medium_1024":
             return cpu_baseline_sd35(res["_cfg"], res["_n_img"], WORKLOADS[name]["text_len"], threads)
+        if name == "sd35_packed_2x1024_4x512":
+            wl = WORKLOADS[name]
+            return cpu_baseline_sd35_packed(res["_cfg"], wl["sizes"], wl["text_len"], threads)
         if name == "wan21_packed_4req":
             from ditserve_amd.wan import WAN21_T2V_1_3B
             return cpu_baseline_wan_packed(WAN21_T2V_1_3B, res["_grids"], threads)
@@ -498,7 +684,7 @@ def main():
         "config": {"workload": head["workload"], "tokens_per_step": head["tokens_per_step"],
                    "blocks": head["blocks"]},
         "tokens_per_s": head["tokens_per_s"], "model_tflops": head["model_tflops"],
-        "model_mfma_frac": head["model_mfma_frac"], "roofline": head["roofline"],
+        "model_mfma_frac": head["model_mfma_frac"], "roofline": head["roofline"], "kernels": head["kernels"],
         "reference_a100_ms_per_step": head["reference_a100_ms_per_step"],
     }
     if "breakdown_ms_per_step" in head:
@@ -508,7 +694,7 @@ def main():
     if not args.no_per_config:
         per = {}
         plan = [("wan21_480p", 3, 1), ("wan21_packed_4req", 5, 2), ("sd35_medium_1024", 10, 3),
-                ("wan22_ti2v_5b_704p", 3, 1)]
+                ("sd35_packed_2x1024_4x512", 5, 2), ("wan22_ti2v_5b_704p", 3, 1)]
         for name, steps, warmup in plan:
             if name == args.workload:
                 res = dict(head)
@@ -521,6 +707,7 @@ def main():
                     res["cpu_baseline"] = cpu_for(name, res)
             key = {"wan21_480p": "wan21_480p_cfg2", "wan21_packed_4req": "wan21_packed_4req",
                    "sd35_medium_1024": "sd35_medium_1024_cfg2",
+                   "sd35_packed_2x1024_4x512": "sd35_packed_2x1024_4x512_cfg2",
                    "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2"}[name]
             res.pop("breakdown_ms_per_step", None)
             per[key] = _public(res)

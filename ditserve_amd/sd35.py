@@ -263,14 +263,16 @@ class SD35Transformer:
         D, H, Dh = self.cfg.dim, self.cfg.heads, self.cfg.head_dim
         q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
         ops.qk_norm_rope_(q, k, wq, wk, Dh, self.cfg.eps, per_head=True)
-        return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh, q_prescaled=True)
+        with self.profiler.region("attn_dual_core"):
+            return ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh, q_prescaled=True)
 
     def _block(self, i, h, c, mod, seg_img, seg_txt, seg_joint):
         cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
         D, eps = cfg.dim, cfg.eps
         with prof.region("adaln"):
             emb = mod[:, slice(*blk["n1_cols"])]  # [M, 6D or 9D]
-            nh = ops.adaln(h, emb[:, 0:D], emb[:, D:2 * D], seg_img, eps=eps)
+            with prof.region("adaln_img"):
+                nh = ops.adaln(h, emb[:, 0:D], emb[:, D:2 * D], seg_img, eps=eps)
             nh2 = ops.adaln(h, emb[:, 6 * D:7 * D], emb[:, 7 * D:8 * D], seg_img, eps=eps) if blk["dual"] else None
             embc = mod[:, slice(*blk["n1c_cols"])]  # [M, 2D] (last) or [M, 6D]
             if blk["last"]:  # AdaLN-Continuous: (scale, shift)
@@ -278,17 +280,21 @@ class SD35Transformer:
             else:
                 nc = ops.adaln(c, embc[:, 0:D], embc[:, D:2 * D], seg_txt, eps=eps)
         with prof.region("gemm_qkv"):
-            qkv_i = ops.linear(nh, *blk["qkv"])
-            qkv_t = ops.linear(nc, *blk["qkv_t"])
+            with prof.region("gemm_qkv_img"):
+                qkv_i = ops.linear(nh, *blk["qkv"])
+            with prof.region("gemm_qkv_txt"):
+                qkv_t = ops.linear(nc, *blk["qkv_t"])
         with prof.region("joint_prep"):
             D3 = 3 * D
-            ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq_pre"], blk["nk"], cfg.head_dim, eps,
-                              per_head=True)
+            with prof.region("qk_norm_img"):
+                ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq_pre"], blk["nk"], cfg.head_dim, eps,
+                                  per_head=True)
             ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt_pre"], blk["nkt"], cfg.head_dim, eps,
                               per_head=True)
             # image and text rows are read in place: no gather / scatter copies
-            vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
-                                       seg_img, seg_txt, seg_joint)
+            with prof.region("transpose_v_joint"):
+                vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
+                                           seg_img, seg_txt, seg_joint)
         with prof.region("attn_joint"):
             a_img, a_txt = ops.joint_attention_q_prescaled(
                 qkv_i[:, :D], qkv_t[:, :D], qkv_i[:, D:2 * D], qkv_t[:, D:2 * D], vt, seg_img, seg_txt,
@@ -299,8 +305,9 @@ class SD35Transformer:
             if blk["last"]:
                 h = ops.linear(epilogue="gate_res", **img)
             else:  # image and text output projections, one launch where that pays
-                h, c = ops.linear_pair(img, dict(x=a_txt, w=blk["out_t"][0], b=blk["out_t"][1], residual=c,
-                                                 gate=embc[:, 2 * D:3 * D], segments=seg_txt), "gate_res")
+                with prof.region("gemm_out_pair"):
+                    h, c = ops.linear_pair(img, dict(x=a_txt, w=blk["out_t"][0], b=blk["out_t"][1], residual=c,
+                                                     gate=embc[:, 2 * D:3 * D], segments=seg_txt), "gate_res")
         if blk["dual"]:
             with prof.region("attn_dual"):
                 qkv2 = ops.linear(nh2, *blk["qkv2"])
@@ -308,7 +315,8 @@ class SD35Transformer:
                 ops.linear(a2, *blk["out2"], "gate_res", residual=h, gate=emb[:, 8 * D:9 * D], segments=seg_img, out=h)
         with prof.region("ffn"):
             n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)
-            fx = ops.linear(n2, *blk["ff1"], "gelu")
+            with prof.region("gemm_ffn_up_img"):
+                fx = ops.linear(n2, *blk["ff1"], "gelu")
             img = dict(x=fx, w=blk["ff2"][0], b=blk["ff2"][1], residual=h, gate=emb[:, 5 * D:6 * D],
                        segments=seg_img, out=h)
             if blk["last"]:
@@ -316,8 +324,9 @@ class SD35Transformer:
                 return h, None
             n2c = ops.adaln(c, embc[:, 3 * D:4 * D], embc[:, 4 * D:5 * D], seg_txt, eps=eps)
             fc = ops.linear(n2c, *blk["ffc1"], "gelu")
-            ops.linear_pair(img, dict(x=fc, w=blk["ffc2"][0], b=blk["ffc2"][1], residual=c,
-                                      gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c), "gate_res")
+            with prof.region("gemm_ffn_down_pair"):
+                ops.linear_pair(img, dict(x=fc, w=blk["ffc2"][0], b=blk["ffc2"][1], residual=c,
+                                          gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c), "gate_res")
         return h, c
 
     # ------------------------------------------------------------------ forward

@@ -676,6 +676,8 @@ def main():
         return cpu_baseline_wan_step(res["_cfg"], res["_grid"], threads, label)
 
     head = headline_for(args.workload, args.steps, args.warmup, calibrate=args.workload == "wan21_480p")
+    print(f"[bench] {args.workload}: {head['ms_per_step']:.2f} ms/step over {args.steps} steps", file=sys.stderr,
+          flush=True)
     out = {
         "metric": head["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
@@ -711,6 +713,7 @@ def main():
                    "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2"}[name]
             res.pop("breakdown_ms_per_step", None)
             per[key] = _public(res)
+            print(f"[bench] {key}: {res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
         _release()
         blk = run_wan_block()
         if cpu:

@@ -36,6 +36,7 @@ on one full-shape block-forward and extrapolates to the step (blocks x branches)
 """
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -81,6 +82,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-per-config", action="store_true", help="headline workload only")
     ap.add_argument("--breakdown", action="store_true", help="per-op HIP-event breakdown in the JSON")
+    ap.add_argument("--surfaces", action="store_true",
+                    help="only time the reference-shaped entry points against the engine path (one JSON line)")
     ap.add_argument("--workload", default="wan21_480p", choices=sorted(WORKLOADS),
                     help="the workload of the top-level line (default: the Wan2.1 480p headline)")
     return ap.parse_args()
@@ -363,7 +366,16 @@ def _release():
     torch.cuda.empty_cache()
 
 
-def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
+def calibration_copy():
+    """The known-size copy (CALIB_BYTES read and written, outside any timing) that
+    the HBM-traffic counters of a profile of this script are scaled by."""
+    import torch
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device="cuda")
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+
+
+def run_wan_cfg(name, steps, warmup, breakdown=False):
     """Wan CFG-pair denoise step (Wan2.1 480p or Wan2.2-5B 704p)."""
     import torch
 
@@ -396,11 +408,6 @@ def run_wan_cfg(name, steps, warmup, breakdown=False, calibrate=False):
     latent, ms, regions, kregions = _timed(step, latent, steps, warmup, model, {"attn_self"}, breakdown)
     if not bool(torch.isfinite(latent).all()):
         raise RuntimeError(f"{name}: non-finite latent after the timed steps")
-    if calibrate:
-        # the known-size copy the HBM-traffic counters are scaled by (outside timing)
-        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
-        torch.empty_like(src).copy_(src)
-        torch.cuda.synchronize()
     attn_flops = 4.0 * 2 * seq * seq * cfg.dim  # per launch: 2 segments (CFG pair), non-causal
     total_flops = step_flops(cfg, [seq, seq], cfg.text_len)
     arch = "Wan2.1-T2V-1.3B" if wl["arch"] == "wan21" else "Wan2.2-TI2V-5B"
@@ -604,6 +611,89 @@ def run_sd35_packed(steps, warmup, breakdown=False):
     return out
 
 
+def run_surfaces(repeats=10):
+    """GPU time of the reference-shaped entry points against the engine's own
+    kernel sequence for the same work, at the Wan2.1 480p CFG-pair shape (2 x 32760
+    tokens, 12 heads x 128) and the SD3.5-M 1024^2 CFG-pair joint shape (2 x (4096 +
+    333) tokens, 24 heads x 64).  Each figure is the average of `repeats` calls
+    bracketed by HIP events on the current stream (host overhead included where a
+    call leaves the GPU idle)."""
+    import torch
+
+    from ditserve_amd import attention, ops
+    from ditserve_amd.wan import fused_qk_norm_rope
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * scale).to(torch.bfloat16)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(repeats):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / repeats
+
+    out = {}
+    # Wan self-attention of one block: QK-norm + RoPE, V staging, attention
+    B, S, H, D = 2, 32760, 12, 128
+    qkv = rnd(B * S, 3 * H * D)
+    wq = torch.ones(H * D, device=dev)
+    cos, sin = torch.ones(1, S, 1, D, device=dev), torch.zeros(1, S, 1, D, device=dev)
+    seg = ops.Segments([0, S, 2 * S], dev)
+    rope = ops.Rope(cos.reshape(S, D)[:, 0::2].contiguous(), sin.reshape(S, D)[:, 1::2].contiguous(),
+                    [(S, 1, 1)] * B, seg, D // 2, 0)
+    q, k, v = qkv[:, :H * D], qkv[:, H * D:2 * H * D], qkv[:, 2 * H * D:]
+
+    # the engine's q norm weight carries softmax_scale * log2(e) (the pre-scaled kernel's q)
+    wq_pre = wq * (ops.LOG2E / math.sqrt(D))
+
+    def engine():
+        ops.qk_norm_rope_(q, k, wq_pre, wq, D, 1e-6, rope=rope)
+        vt = ops.transpose_v(v, H, D, seg)
+        return ops.flash_attn_varlen(q, k, None, seg, seg, H, D, vt=vt, q_prescaled=True)
+    out["wan_self_engine_ms"] = timed(engine)
+    qb, kb, vb = (x.reshape(B, S, H * D) for x in (q.contiguous(), k.contiguous(), v.contiguous()))
+
+    def plugin():
+        # the reference's processor: slot -> BHSD views -> attention backend -> [B, S, H*D]
+        qq, kk = fused_qk_norm_rope(qb, kb, wq, wq, cos, sin, H)
+        o, _ = attention.ditk_attention(qq.transpose(1, 2), kk.transpose(1, 2),
+                                        vb.view(B, S, H, D).transpose(1, 2), attention.AttnCall())
+        return o.transpose(1, 2).flatten(2, 3)
+    out["wan_self_reference_surface_ms"] = timed(plugin)
+    out["wan_fused_qk_norm_rope_slot_ms"] = timed(lambda: fused_qk_norm_rope(qb, kb, wq, wq, cos, sin, H))
+    out["wan_qk_norm_rope_in_place_ms"] = timed(lambda: ops.qk_norm_rope_(q, k, wq, wq, D, 1e-6, rope=rope))
+    del qkv, q, k, v, qb, kb, vb
+    _release()
+    # SD3.5 joint attention: engine (in-place sources) vs the varlen slot on gathered joint rows
+    H2, D2, n, l = 24, 64, 4096, 333
+    qi, ki, vi = rnd(2 * n, H2 * D2, scale=0.18), rnd(2 * n, H2 * D2), rnd(2 * n, H2 * D2)
+    qt, kt, vtx = rnd(2 * l, H2 * D2, scale=0.18), rnd(2 * l, H2 * D2), rnd(2 * l, H2 * D2)
+    si, st, sj = ops.Segments([0, n, 2 * n], dev), ops.Segments([0, l, 2 * l], dev), \
+        ops.Segments([0, n + l, 2 * (n + l)], dev)
+
+    def joint_engine():
+        vt = ops.transpose_v_joint(vi, vtx, H2, D2, si, st, sj)
+        return ops.joint_attention_q_prescaled(qi, qt, ki, kt, vt, si, st, sj, H2, D2)
+    out["sd35_joint_engine_ms"] = timed(joint_engine)
+    cat = lambda a, b: torch.cat([a[:n], b[:l], a[n:], b[l:]]).view(-1, H2, D2)  # noqa: E731
+    jq, jk, jv = cat(qi, qt), cat(ki, kt), cat(vi, vtx)
+    cu = torch.tensor([0, n + l, 2 * (n + l)], dtype=torch.int32, device=dev)
+    out["sd35_varlen_slot_ms"] = timed(lambda: attention.flash_attn_varlen_func(jq, jk, jv, cu, cu, n + l, n + l))
+    attention.check_tables()
+    return {"metric": "reference-surface entry points vs the engine path (GPU ms per call)", "unit": "ms",
+            "higher_is_better": False, "repeats": repeats, **{k: round(v, 4) for k, v in out.items()},
+            "workload": "Wan2.1 480p CFG pair (2 x 32760 tokens, 12 x 128) self-attention with QK-norm + RoPE; "
+                        "SD3.5-M 1024^2 CFG pair joint attention (2 x (4096 + 333) tokens, 24 x 64)"}
+
+
 def run_wan_block(repeats=20):
     """One Wan2.1 block on the 1x30x52 grid (1560 tokens, 77 valid text rows, t=500)."""
     import torch
@@ -650,17 +740,20 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.surfaces:
+        print(json.dumps(run_surfaces()), flush=True)
+        return
     threads = cpu_threads()
     cpu = not args.no_cpu_baseline
 
-    def headline_for(name, steps, warmup, calibrate=False):
+    def headline_for(name, steps, warmup):
         if name == "sd35_medium_1024":
             return run_sd35(steps, warmup, args.breakdown)
         if name == "sd35_packed_2x1024_4x512":
             return run_sd35_packed(steps, warmup, args.breakdown)
         if name == "wan21_packed_4req":
             return run_wan_packed(steps, warmup, args.breakdown)
-        return run_wan_cfg(name, steps, warmup, args.breakdown, calibrate)
+        return run_wan_cfg(name, steps, warmup, args.breakdown)
 
     def cpu_for(name, res):
         torch.set_num_threads(threads)
@@ -675,7 +768,8 @@ def main():
         label = "Wan2.1" if WORKLOADS[name]["arch"] == "wan21" else "Wan2.2-5B"
         return cpu_baseline_wan_step(res["_cfg"], res["_grid"], threads, label)
 
-    head = headline_for(args.workload, args.steps, args.warmup, calibrate=args.workload == "wan21_480p")
+    head = headline_for(args.workload, args.steps, args.warmup)
+    calibration_copy()
     print(f"[bench] {args.workload}: {head['ms_per_step']:.2f} ms/step over {args.steps} steps", file=sys.stderr,
           flush=True)
     out = {

@@ -351,8 +351,7 @@ def _sd35_kernel_spec(cfg, img_counts, txt_counts):
         "gemm_ffn_up_img": ("mfma", 2.0 * Mi * F * D, f"image FFN up {Mi}x{F}x{D}, GELU-tanh"),
         "gemm_ffn_down_pair": ("mfma", 2.0 * (Mi + Mt) * D * F,
                                f"image + text FFN down ({Mi} + {Mt})x{D}x{F}, gated residual, one pair call"),
-        "adaln_img": ("hbm", 4.0 * Mi * D, "image AdaLN-Zero (LayerNorm + per-segment shift/scale)"),
-        "qk_norm_img": ("hbm", 8.0 * Mi * D, "image per-head QK RMSNorm, in place on q and k"),
+        "qk_norm": ("hbm", 8.0 * (Mi + Mt) * D, "image and text per-head QK RMSNorm, in place on q and k, one launch"),
         "transpose_v_joint": ("hbm", 4.0 * (Mi + Mt) * D, "image + text V -> joint transposed Vt staging"),
     }
 

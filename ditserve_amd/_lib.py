@@ -15,6 +15,20 @@ LIB_PATH = pathlib.Path(os.environ.get("DITK_LIB", _PKG / "libditk.so"))
 c_void_p, c_int, c_int64, c_float = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 _P = c_void_p
 
+
+class AdalnJob(ctypes.Structure):
+    """ditk_adaln_job of include/ditk.h."""
+    _fields_ = [("x", _P), ("ldx", c_int64), ("y", _P), ("ldy", c_int64), ("cu_seqlens", _P), ("shift", _P),
+                ("scale", _P), ("mod_stride", c_int64), ("weight", _P), ("bias", _P), ("T", c_int), ("D", c_int),
+                ("nseg", c_int), ("norm_kind", c_int), ("eps", c_float)]
+
+
+class QkNormJob(ctypes.Structure):
+    """ditk_qk_norm_job of include/ditk.h."""
+    _fields_ = [("q", _P), ("ldq", c_int64), ("k", _P), ("ldk", c_int64), ("q_out", _P), ("ldqo", c_int64),
+                ("k_out", _P), ("ldko", c_int64), ("wq", _P), ("wk", _P), ("T", c_int), ("D", c_int),
+                ("head_dim", c_int), ("per_head", c_int), ("eps", c_float)]
+
 # name -> (restype, argtypes).  Mirrors include/ditk.h.
 SIGNATURES = {
     "ditk_version": (c_int, []),
@@ -46,6 +60,8 @@ SIGNATURES = {
     "ditk_cfg_combine": (c_int, [_P, _P, _P, c_int64, c_float, _P]),
     "ditk_joint_copy": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "ditk_silu": (c_int, [_P, _P, c_int64, _P]),
+    "ditk_adaln_multi": (c_int, [ctypes.POINTER(AdalnJob), c_int, _P]),
+    "ditk_qk_norm_multi": (c_int, [ctypes.POINTER(QkNormJob), c_int, _P]),
     "ditk_check_cu_seqlens": (c_int, [_P, c_int, c_int, _P, _P, _P]),
     "ditk_solver_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P]),
     "ditk_flash_attn_varlen_noalloc": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64,

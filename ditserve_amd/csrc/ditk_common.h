@@ -28,6 +28,40 @@ typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 void ditk_set_error(const char* fmt, ...);
 int ditk_check_launch(const char* what);
 
+// Jobs of the multi-job row-kernel entry points; the same layout as the
+// declarations of include/ditk.h (C ABI).
+struct ditk_adaln_job {
+  const void* x;
+  int64_t ldx;
+  void* y;
+  int64_t ldy;
+  const int32_t* cu_seqlens;
+  const float* shift;
+  const float* scale;
+  int64_t mod_stride;
+  const float* weight;
+  const float* bias;
+  int T, D, nseg, norm_kind;
+  float eps;
+};
+static_assert(sizeof(ditk_adaln_job) == 104, "ditk_adaln_job layout");
+
+struct ditk_qk_norm_job {
+  const void* q;
+  int64_t ldq;
+  const void* k;
+  int64_t ldk;
+  void* q_out;
+  int64_t ldqo;
+  void* k_out;
+  int64_t ldko;
+  const float* wq;
+  const float* wk;
+  int T, D, head_dim, per_head;
+  float eps;
+};
+static_assert(sizeof(ditk_qk_norm_job) == 104, "ditk_qk_norm_job layout");
+
 #define DITK_REQUIRE(cond, ...)        \
   do {                                 \
     if (!(cond)) {                     \

@@ -18,14 +18,12 @@ constexpr int kMaxChunks = 8;     // 16-byte chunks per lane -> D <= 64*8*8 = 40
 //   norm = LayerNorm (kind 0) or RMSNorm (kind 1), eps inside the rsqrt.
 // ---------------------------------------------------------------------------
 template <int KIND, int NC>
-__global__ __launch_bounds__(256) void adaln_kernel(
-    const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int T, int D,
+__device__ __forceinline__ void adaln_row(
+    const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int row, int D,
     const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
     const float* __restrict__ scale, int64_t mod_stride, const float* __restrict__ w,
     const float* __restrict__ b, float eps) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= T) return;
   const int nchunk = D >> 3;
   const bf16_t* xr = x + (int64_t)row * ldx;
   // Every load of the row is issued before the reductions: the row itself
@@ -120,6 +118,52 @@ __global__ __launch_bounds__(256) void adaln_kernel(
   }
 }
 
+template <int KIND, int NC>
+__global__ __launch_bounds__(256) void adaln_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int T, int D,
+    const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
+    const float* __restrict__ scale, int64_t mod_stride, const float* __restrict__ w,
+    const float* __restrict__ b, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= T) return;
+  adaln_row<KIND, NC>(x, ldx, y, ldy, row, D, cu, nseg, shift, scale, mod_stride, w, b, eps);
+}
+
+// Several AdaLN jobs of one norm kind and chunk count in one launch: job j owns
+// workgroups [block0[j], block0[j + 1]), four rows each, and runs adaln_row on
+// its own tensors, so each row is computed exactly as a single-job launch would.
+constexpr int kMaxJobs = 4;
+struct AdalnJob {
+  const bf16_t* x;
+  int64_t ldx;
+  bf16_t* y;
+  int64_t ldy;
+  const int32_t* cu;
+  const float* shift;
+  const float* scale;
+  int64_t mod_stride;
+  const float* w;
+  const float* b;
+  int T, D, nseg;
+  float eps;
+};
+struct AdalnJobs {
+  AdalnJob job[kMaxJobs];
+  int block0[kMaxJobs + 1];
+  int njobs;
+};
+
+template <int KIND, int NC>
+__global__ __launch_bounds__(256) void adaln_multi_kernel(AdalnJobs jobs) {
+  int j = 0;
+  while (j + 1 < jobs.njobs && (int)blockIdx.x >= jobs.block0[j + 1]) ++j;
+  const AdalnJob& a = jobs.job[j];
+  const int row = ((int)blockIdx.x - jobs.block0[j]) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= a.T) return;
+  adaln_row<KIND, NC>(a.x, a.ldx, a.y, a.ldy, row, a.D, a.cu, a.nseg, a.shift, a.scale, a.mod_stride, a.w, a.b,
+                      a.eps);
+}
+
 // mod[s, j, d] = table[j, d] + proj[s, j, d]   (fp32; k rows of D per segment)
 __global__ void modulation_kernel(const float* __restrict__ table, const float* __restrict__ proj,
                                   float* __restrict__ mod, int nseg, int kd) {
@@ -209,9 +253,9 @@ __device__ __forceinline__ void norm_rotate_store(bf16_t* __restrict__ xr, const
 }
 
 template <int GROUP_LANES, int NC>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+__device__ __forceinline__ void qk_norm_row(
     const bf16_t* q, int64_t ldq, const bf16_t* k, int64_t ldk, bf16_t* qo, int64_t ldqo, bf16_t* ko,
-    int64_t ldko, int T, int D,
+    int64_t ldko, int row, int D,
     int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
     const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
@@ -220,8 +264,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   // the rows (before the reductions), above that after them to bound registers.
   constexpr bool kEarlyW = NC <= 4;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= T) return;
   // q/k may be the outputs themselves (in place): a lane reads its row chunks
   // before it writes them, and no other lane touches them
   const bf16_t* qr = q + (int64_t)row * ldq;
@@ -281,13 +323,48 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   norm_rotate_store<NC>(ko + (int64_t)row * ldko, rawk, rsk, wk4, rope, rc, rsn, nchunk, lane);
 }
 
+template <int GROUP_LANES, int NC>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const bf16_t* q, int64_t ldq, const bf16_t* k, int64_t ldk, bf16_t* qo, int64_t ldqo, bf16_t* ko,
+    int64_t ldko, int T, int D,
+    int head_dim, const float* __restrict__ wq, const float* __restrict__ wk, float eps,
+    const float* __restrict__ rcos, const float* __restrict__ rsin, int max_pos,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ grids, int nseg, int t_pairs,
+    int h_pairs) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= T) return;
+  qk_norm_row<GROUP_LANES, NC>(q, ldq, k, ldk, qo, ldqo, ko, ldko, row, D, head_dim, wq, wk, eps, rcos, rsin,
+                               max_pos, cu, grids, nseg, t_pairs, h_pairs);
+}
+
+// Several RoPE-free QK-norm jobs of one group width and chunk count in one
+// launch (SD3.5's image and text per-head norms): job j owns workgroups
+// [block0[j], block0[j + 1]) and runs qk_norm_row on its own tensors.
+struct QkNormJobs {
+  ditk_qk_norm_job job[kMaxJobs];
+  int block0[kMaxJobs + 1];
+  int njobs;
+};
+
+template <int GROUP_LANES, int NC>
+__global__ __launch_bounds__(256) void qk_norm_multi_kernel(QkNormJobs jobs) {
+  int j = 0;
+  while (j + 1 < jobs.njobs && (int)blockIdx.x >= jobs.block0[j + 1]) ++j;
+  const ditk_qk_norm_job& a = jobs.job[j];
+  const int row = ((int)blockIdx.x - jobs.block0[j]) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= a.T) return;
+  qk_norm_row<GROUP_LANES, NC>((const bf16_t*)a.q, a.ldq, (const bf16_t*)a.k, a.ldk, (bf16_t*)a.q_out, a.ldqo,
+                               (bf16_t*)a.k_out, a.ldko, row, a.D, a.head_dim, a.wq, a.wk, a.eps, nullptr, nullptr,
+                               0, nullptr, nullptr, 0, 0, 0);
+}
+
 }  // namespace
 
-DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D,
-                           const int32_t* cu_seqlens, int nseg, const float* shift,
-                           const float* scale, int64_t mod_stride, const float* weight,
-                           const float* bias, float eps, int norm_kind, hipStream_t stream) {
-  DITK_REQUIRE(x != nullptr && y != nullptr, "ditk_adaln: null tensor");
+namespace {
+int adaln_check(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D, const int32_t* cu_seqlens, int nseg,
+                const float* shift, const float* scale, int64_t mod_stride, const float* weight, const float* bias,
+                int norm_kind) {
+  DITK_REQUIRE(T == 0 || (x != nullptr && y != nullptr), "ditk_adaln: null tensor");
   DITK_REQUIRE(T >= 0 && D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks,
                "ditk_adaln: D=%d must be a positive multiple of 8 and <= %d", D, 64 * 8 * kMaxChunks);
   DITK_REQUIRE(ldx % 8 == 0 && ldy % 8 == 0 && ldx >= D && ldy >= D,
@@ -300,6 +377,17 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
   DITK_REQUIRE(shift == nullptr || (cu_seqlens != nullptr && nseg > 0),
                "ditk_adaln: modulation needs cu_seqlens");
   DITK_REQUIRE(norm_kind == 0 || norm_kind == 1, "ditk_adaln: norm_kind must be 0 (LN) or 1 (RMS)");
+  return 0;
+}
+}  // namespace
+
+DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D,
+                           const int32_t* cu_seqlens, int nseg, const float* shift,
+                           const float* scale, int64_t mod_stride, const float* weight,
+                           const float* bias, float eps, int norm_kind, hipStream_t stream) {
+  const int rc = adaln_check(x, ldx, y, ldy, T, D, cu_seqlens, nseg, shift, scale, mod_stride, weight, bias,
+                             norm_kind);
+  if (rc) return rc;
   if (T == 0) return 0;
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
@@ -327,6 +415,53 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
   return ditk_check_launch("ditk_adaln");
 }
 
+DITK_EXPORT int ditk_adaln_multi(const ditk_adaln_job* jobs, int njobs, hipStream_t stream) {
+  DITK_REQUIRE(jobs != nullptr && njobs >= 1 && njobs <= kMaxJobs, "ditk_adaln_multi: 1 to %d jobs", kMaxJobs);
+  AdalnJobs a = {};
+  a.njobs = njobs;
+  int nc = 0, kind = 0;
+  int64_t blocks = 0;
+  for (int j = 0; j < njobs; ++j) {
+    const ditk_adaln_job& p = jobs[j];
+    const int rc = adaln_check(p.x, p.ldx, p.y, p.ldy, p.T, p.D, p.cu_seqlens, p.nseg, p.shift, p.scale,
+                               p.mod_stride, p.weight, p.bias, p.norm_kind);
+    if (rc) return rc;
+    const int ncj = (p.D / 8 + 63) / 64;
+    DITK_REQUIRE(j == 0 || (ncj == nc && p.norm_kind == kind),
+                 "ditk_adaln_multi: jobs must share the norm kind and ceil(D / 512)");
+    nc = ncj;
+    kind = p.norm_kind;
+    a.job[j] = AdalnJob{(const bf16_t*)p.x, p.ldx, (bf16_t*)p.y, p.ldy, p.cu_seqlens, p.shift, p.scale,
+                        p.mod_stride, p.weight, p.bias, p.T, p.D, p.nseg, p.eps};
+    a.block0[j] = (int)blocks;
+    blocks += (p.T + kRowsPerBlock - 1) / kRowsPerBlock;
+  }
+  DITK_REQUIRE(blocks < (1ll << 31), "ditk_adaln_multi: too many rows");
+  a.block0[njobs] = (int)blocks;
+  if (blocks == 0) return 0;
+  const dim3 grid((unsigned)blocks);
+#define DITK_ADALN_M(K, NCV) adaln_multi_kernel<K, NCV><<<grid, 256, 0, stream>>>(a)
+#define DITK_ADALN_M_NC(K)              \
+  switch (nc) {                         \
+    case 1: DITK_ADALN_M(K, 1); break;  \
+    case 2: DITK_ADALN_M(K, 2); break;  \
+    case 3: DITK_ADALN_M(K, 3); break;  \
+    case 4: DITK_ADALN_M(K, 4); break;  \
+    case 5: DITK_ADALN_M(K, 5); break;  \
+    case 6: DITK_ADALN_M(K, 6); break;  \
+    case 7: DITK_ADALN_M(K, 7); break;  \
+    default: DITK_ADALN_M(K, 8); break; \
+  }
+  if (kind == 0) {
+    DITK_ADALN_M_NC(0)
+  } else {
+    DITK_ADALN_M_NC(1)
+  }
+#undef DITK_ADALN_M_NC
+#undef DITK_ADALN_M
+  return ditk_check_launch("ditk_adaln_multi");
+}
+
 DITK_EXPORT int ditk_modulation(const float* table, const float* proj, float* mod, int nseg, int kd,
                                 hipStream_t stream) {
   DITK_REQUIRE(table && proj && mod && nseg > 0 && kd > 0, "ditk_modulation: bad arguments");
@@ -336,11 +471,10 @@ DITK_EXPORT int ditk_modulation(const float* table, const float* proj, float* mo
 }
 
 namespace {
-int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, void* qo, int64_t ldqo, void* ko,
-                        int64_t ldko, int T, int D, int head_dim, const float* wq, const float* wk, float eps,
-                        int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
-                        const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
-                        hipStream_t stream) {
+int qk_norm_check(const void* q, int64_t ldq, const void* k, int64_t ldk, void* qo, int64_t ldqo, void* ko,
+                  int64_t ldko, int D, int head_dim, const float* wq, const float* wk, const float* rope_cos,
+                  const float* rope_sin, int max_pos, const int32_t* cu_seqlens, const int32_t* grids, int nseg,
+                  int t_pairs, int h_pairs) {
   DITK_REQUIRE(q && k && qo && ko && wq && wk, "ditk_qk_norm_rope: null tensor");
   DITK_REQUIRE(D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks, "ditk_qk_norm_rope: bad D=%d", D);
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_qk_norm_rope: head_dim must be 64 or 128");
@@ -358,6 +492,18 @@ int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, 
                "ditk_qk_norm_rope: the middle axis must own 0 or >= 4 pairs");
   DITK_REQUIRE(rope_cos == nullptr || (((uintptr_t)rope_cos % 16) == 0 && ((uintptr_t)rope_sin % 16) == 0),
                "ditk_qk_norm_rope: RoPE tables must be 16-byte aligned");
+  return 0;
+}
+
+int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, void* qo, int64_t ldqo, void* ko,
+                        int64_t ldko, int T, int D, int head_dim, const float* wq, const float* wk, float eps,
+                        int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
+                        const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
+                        hipStream_t stream) {
+  const int rc = qk_norm_check(q, ldq, k, ldk, qo, ldqo, ko, ldko, D, head_dim, wq, wk, rope_cos, rope_sin, max_pos,
+                               cu_seqlens, grids, nseg, t_pairs, h_pairs);
+  if (rc) return rc;
+  DITK_REQUIRE(T >= 0, "ditk_qk_norm_rope: bad T");
   if (T == 0) return 0;
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
@@ -389,6 +535,56 @@ int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, 
   return ditk_check_launch("ditk_qk_norm_rope");
 }
 }  // namespace
+
+DITK_EXPORT int ditk_qk_norm_multi(const ditk_qk_norm_job* jobs, int njobs, hipStream_t stream) {
+  DITK_REQUIRE(jobs != nullptr && njobs >= 1 && njobs <= kMaxJobs, "ditk_qk_norm_multi: 1 to %d jobs", kMaxJobs);
+  QkNormJobs a = {};
+  a.njobs = njobs;
+  int nc = 0, group = 0;
+  int64_t blocks = 0;
+  for (int j = 0; j < njobs; ++j) {
+    const ditk_qk_norm_job& p = jobs[j];
+    const int rc = qk_norm_check(p.q, p.ldq, p.k, p.ldk, p.q_out, p.ldqo, p.k_out, p.ldko, p.D, p.head_dim, p.wq,
+                                 p.wk, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0);
+    if (rc) return rc;
+    DITK_REQUIRE(p.T >= 0, "ditk_qk_norm_multi: bad T");
+    const int ncj = (p.D / 8 + 63) / 64;
+    const int gj = !p.per_head ? 64 : (p.head_dim == 128 ? 16 : 8);
+    DITK_REQUIRE(j == 0 || (ncj == nc && gj == group),
+                 "ditk_qk_norm_multi: jobs must share ceil(D / 512) and the norm grouping (per head and head_dim)");
+    nc = ncj;
+    group = gj;
+    a.job[j] = p;
+    a.block0[j] = (int)blocks;
+    blocks += (p.T + kRowsPerBlock - 1) / kRowsPerBlock;
+  }
+  DITK_REQUIRE(blocks < (1ll << 31), "ditk_qk_norm_multi: too many rows");
+  a.block0[njobs] = (int)blocks;
+  if (blocks == 0) return 0;
+  const dim3 grid((unsigned)blocks);
+#define DITK_QKM(G, NCV) qk_norm_multi_kernel<G, NCV><<<grid, 256, 0, stream>>>(a)
+#define DITK_QKM_NC(G)              \
+  switch (nc) {                     \
+    case 1: DITK_QKM(G, 1); break;  \
+    case 2: DITK_QKM(G, 2); break;  \
+    case 3: DITK_QKM(G, 3); break;  \
+    case 4: DITK_QKM(G, 4); break;  \
+    case 5: DITK_QKM(G, 5); break;  \
+    case 6: DITK_QKM(G, 6); break;  \
+    case 7: DITK_QKM(G, 7); break;  \
+    default: DITK_QKM(G, 8); break; \
+  }
+  if (group == 64) {
+    DITK_QKM_NC(64)
+  } else if (group == 16) {
+    DITK_QKM_NC(16)
+  } else {
+    DITK_QKM_NC(8)
+  }
+#undef DITK_QKM_NC
+#undef DITK_QKM
+  return ditk_check_launch("ditk_qk_norm_multi");
+}
 
 DITK_EXPORT int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D,
                                   int head_dim, const float* wq, const float* wk, float eps,

@@ -201,6 +201,24 @@ def adaln(x, shift=None, scale=None, segments=None, weight=None, bias=None, eps=
 
     x [T, D] bf16; shift/scale fp32 views [nseg, D] (row stride may exceed D);
     weight/bias fp32 [D]; kind "ln" (LayerNorm) or "rms" (RMSNorm)."""
+    out, job = _adaln_job(x, shift, scale, segments, weight, bias, eps, kind, out)
+    _lib.call("ditk_adaln", job.x, job.ldx, job.y, job.ldy, job.T, job.D, job.cu_seqlens, job.nseg, job.shift,
+              job.scale, job.mod_stride, job.weight, job.bias, job.eps, job.norm_kind, _stream())
+    return out
+
+
+def adaln_multi(jobs):
+    """Several adaln() calls (dicts of its keyword arguments, x required) in one
+    launch: 1 to 4 jobs of one kind and one ceil(D / 512).  Returns the outputs;
+    each is bitwise what adaln() returns for its job."""
+    built = [_adaln_job(**j) for j in jobs]
+    arr = (_lib.AdalnJob * len(built))(*[b[1] for b in built])
+    _lib.call("ditk_adaln_multi", arr, len(built), _stream())
+    return [b[0] for b in built]
+
+
+def _adaln_job(x, shift=None, scale=None, segments=None, weight=None, bias=None, eps=1e-6, kind="ln", out=None):
+    """Checks one adaln() call; returns (out, its ditk_adaln_job)."""
     _check(x, "x", _BF16, 2)
     T, D = x.shape
     ldx = _rows(x, "x")
@@ -228,9 +246,11 @@ def adaln(x, shift=None, scale=None, segments=None, weight=None, bias=None, eps=
             _check(t, n, torch.float32, 1)
             if t.shape[0] != D:
                 raise ValueError(f"{n} must be [{D}]")
-    _lib.call("ditk_adaln", _ptr(x), ldx, _ptr(out), ldy, T, D, _ptr(cu), nseg, _ptr(shift), _ptr(scale),
-              mod_stride, _ptr(weight), _ptr(bias), float(eps), {"ln": 0, "rms": 1}[kind], _stream())
-    return out
+    if kind not in ("ln", "rms"):
+        raise ValueError(f"kind must be 'ln' or 'rms', got {kind!r}")
+    job = _lib.AdalnJob(_ptr(x), ldx, _ptr(out), ldy, _ptr(cu), _ptr(shift), _ptr(scale), mod_stride, _ptr(weight),
+                        _ptr(bias), T, D, nseg, {"ln": 0, "rms": 1}[kind], float(eps))
+    return out, job
 
 
 def modulation(table, proj):
@@ -279,6 +299,37 @@ class Rope:
     def record_stream(self, stream):
         for t in self.device_tensors():
             t.record_stream(stream)
+
+
+def qk_norm_multi(jobs):
+    """Several RoPE-free qk_norm_rope_() calls in one launch: jobs are dicts with
+    q, k, wq, wk, head_dim and optionally eps, per_head, out (1 to 4 jobs of one
+    ceil(D / 512), head_dim and per_head).  Each job's result is bitwise what
+    qk_norm_rope_() gives it; returns the (q, k) pairs written."""
+    built, ret = [], []
+    for j in jobs:
+        q, k, wq, wk = j["q"], j["k"], j["wq"], j["wk"]
+        _check(q, "q", _BF16, 2)
+        _check(k, "k", _BF16, 2)
+        if q.shape != k.shape:
+            raise ValueError("q and k must have the same shape")
+        T, D = q.shape
+        for t, n in ((wq, "wq"), (wk, "wk")):
+            _check(t, n, torch.float32, 1)
+            if t.shape[0] != D:
+                raise ValueError(f"{n} must be [{D}]")
+        qo, ko = j.get("out") or (q, k)
+        for t, n in ((qo, "q_out"), (ko, "k_out")):
+            _check(t, n, _BF16, 2)
+            if t.shape != q.shape:
+                raise ValueError(f"{n} must have q's shape {tuple(q.shape)}")
+        built.append(_lib.QkNormJob(_ptr(q), _rows(q, "q"), _ptr(k), _rows(k, "k"), _ptr(qo), _rows(qo, "q_out"),
+                                    _ptr(ko), _rows(ko, "k_out"), _ptr(wq), _ptr(wk), T, D, int(j["head_dim"]),
+                                    int(bool(j.get("per_head", False))), float(j.get("eps", 1e-6))))
+        ret.append((qo, ko))
+    arr = (_lib.QkNormJob * len(built))(*built)
+    _lib.call("ditk_qk_norm_multi", arr, len(built), _stream())
+    return ret
 
 
 def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None, out=None):

@@ -270,15 +270,20 @@ class SD35Transformer:
         cfg, blk, prof = self.cfg, self.blocks[i], self.profiler
         D, eps = cfg.dim, cfg.eps
         with prof.region("adaln"):
+            # image AdaLN-Zero (and the dual branch's), text AdaLN-Zero or, in the last
+            # block, AdaLN-Continuous (scale, shift): one launch
             emb = mod[:, slice(*blk["n1_cols"])]  # [M, 6D or 9D]
-            with prof.region("adaln_img"):
-                nh = ops.adaln(h, emb[:, 0:D], emb[:, D:2 * D], seg_img, eps=eps)
-            nh2 = ops.adaln(h, emb[:, 6 * D:7 * D], emb[:, 7 * D:8 * D], seg_img, eps=eps) if blk["dual"] else None
             embc = mod[:, slice(*blk["n1c_cols"])]  # [M, 2D] (last) or [M, 6D]
-            if blk["last"]:  # AdaLN-Continuous: (scale, shift)
-                nc = ops.adaln(c, embc[:, D:2 * D], embc[:, 0:D], seg_txt, eps=eps)
+            jobs = [dict(x=h, shift=emb[:, 0:D], scale=emb[:, D:2 * D], segments=seg_img, eps=eps)]
+            if blk["last"]:
+                jobs.append(dict(x=c, shift=embc[:, D:2 * D], scale=embc[:, 0:D], segments=seg_txt, eps=eps))
             else:
-                nc = ops.adaln(c, embc[:, 0:D], embc[:, D:2 * D], seg_txt, eps=eps)
+                jobs.append(dict(x=c, shift=embc[:, 0:D], scale=embc[:, D:2 * D], segments=seg_txt, eps=eps))
+            if blk["dual"]:
+                jobs.append(dict(x=h, shift=emb[:, 6 * D:7 * D], scale=emb[:, 7 * D:8 * D], segments=seg_img, eps=eps))
+            normed = ops.adaln_multi(jobs)
+            nh, nc = normed[0], normed[1]
+            nh2 = normed[2] if blk["dual"] else None
         with prof.region("gemm_qkv"):
             with prof.region("gemm_qkv_img"):
                 qkv_i = ops.linear(nh, *blk["qkv"])
@@ -286,11 +291,12 @@ class SD35Transformer:
                 qkv_t = ops.linear(nc, *blk["qkv_t"])
         with prof.region("joint_prep"):
             D3 = 3 * D
-            with prof.region("qk_norm_img"):
-                ops.qk_norm_rope_(qkv_i[:, :D], qkv_i[:, D:2 * D], blk["nq_pre"], blk["nk"], cfg.head_dim, eps,
-                                  per_head=True)
-            ops.qk_norm_rope_(qkv_t[:, :D], qkv_t[:, D:2 * D], blk["nqt_pre"], blk["nkt"], cfg.head_dim, eps,
-                              per_head=True)
+            with prof.region("qk_norm"):  # image and text per-head QK RMSNorm, in place, one launch
+                ops.qk_norm_multi([
+                    dict(q=qkv_i[:, :D], k=qkv_i[:, D:2 * D], wq=blk["nq_pre"], wk=blk["nk"], head_dim=cfg.head_dim,
+                         eps=eps, per_head=True),
+                    dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=blk["nqt_pre"], wk=blk["nkt"],
+                         head_dim=cfg.head_dim, eps=eps, per_head=True)])
             # image and text rows are read in place: no gather / scatter copies
             with prof.region("transpose_v_joint"):
                 vt = ops.transpose_v_joint(qkv_i[:, 2 * D:D3], qkv_t[:, 2 * D:D3], cfg.heads, cfg.head_dim,
@@ -314,7 +320,12 @@ class SD35Transformer:
                 a2 = self._attention(qkv2, seg_img, blk["nq2_pre"], blk["nk2"])
                 ops.linear(a2, *blk["out2"], "gate_res", residual=h, gate=emb[:, 8 * D:9 * D], segments=seg_img, out=h)
         with prof.region("ffn"):
-            n2 = ops.adaln(h, emb[:, 3 * D:4 * D], emb[:, 4 * D:5 * D], seg_img, eps=eps)
+            jobs = [dict(x=h, shift=emb[:, 3 * D:4 * D], scale=emb[:, 4 * D:5 * D], segments=seg_img, eps=eps)]
+            if not blk["last"]:
+                jobs.append(dict(x=c, shift=embc[:, 3 * D:4 * D], scale=embc[:, 4 * D:5 * D], segments=seg_txt,
+                                 eps=eps))
+            normed = ops.adaln_multi(jobs)
+            n2 = normed[0]
             with prof.region("gemm_ffn_up_img"):
                 fx = ops.linear(n2, *blk["ff1"], "gelu")
             img = dict(x=fx, w=blk["ff2"][0], b=blk["ff2"][1], residual=h, gate=emb[:, 5 * D:6 * D],
@@ -322,8 +333,7 @@ class SD35Transformer:
             if blk["last"]:
                 ops.linear(epilogue="gate_res", **img)
                 return h, None
-            n2c = ops.adaln(c, embc[:, 3 * D:4 * D], embc[:, 4 * D:5 * D], seg_txt, eps=eps)
-            fc = ops.linear(n2c, *blk["ffc1"], "gelu")
+            fc = ops.linear(normed[1], *blk["ffc1"], "gelu")
             with prof.region("gemm_ffn_down_pair"):
                 ops.linear_pair(img, dict(x=fc, w=blk["ffc2"][0], b=blk["ffc2"][1], residual=c,
                                           gate=embc[:, 5 * D:6 * D], segments=seg_txt, out=c), "gate_res")

@@ -344,8 +344,9 @@ class WanTransformer:
                 q2 = ops.linear(x, blk["q2_w"], blk["q2_b"])
             kv2 = ops.linear(packet["encoder"], blk["kv2_w"], blk["kv2_b"])
             k2, v2 = kv2[:, :D], kv2[:, D:]
-            ops.adaln(q2, weight=blk["nq2_pre"], eps=cfg.eps, kind="rms", out=q2)
-            ops.adaln(k2, weight=blk["nk2"], eps=cfg.eps, kind="rms", out=k2)
+            # RMSNorm across heads of the image queries and the text keys, in place, one launch
+            ops.adaln_multi([dict(x=q2, weight=blk["nq2_pre"], eps=cfg.eps, kind="rms", out=q2),
+                             dict(x=k2, weight=blk["nk2"], eps=cfg.eps, kind="rms", out=k2)])
             vt2 = ops.transpose_v(v2, H, Dh, seg_txt)
         with prof.region("attn_cross"):
             a = ops.flash_attn_varlen(q2, k2, None, seg, seg_txt, H, Dh, vt=vt2, q_prescaled=True)

@@ -32,7 +32,8 @@ const char* ditk_last_error(void);
  * Fused AdaLN:  y = norm(x) [* weight + bias] [* (1 + scale[seg]) + shift[seg]] -> bf16.
  * norm_kind 0 = LayerNorm (biased variance), 1 = RMSNorm; eps inside rsqrt.
  * shift/scale: fp32 per segment, row stride mod_stride (may be NULL: no modulation).
- * weight/bias: fp32 [D] (may be NULL).  In place (y == x) is allowed.
+ * weight/bias: fp32 [D] (may be NULL).  In place (y == x) is allowed; x and y
+ * may be NULL when T == 0 (nothing is launched).
  * Replaces: Wan AdaLN-1/AdaLN-3 and norm2 — workers/ditserve/models/wan/block.py:283,288,291;
  *   Wan prediction norm_out — block.py:436-446; SD3.5 packed AdaLN-Zero / AdaLN-Continuous —
  *   workers/ditserve/models/sd35_batch.py:336-393; Wan cross-attention norm_q/norm_k
@@ -41,6 +42,31 @@ const char* ditk_last_error(void);
 int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D, const int32_t* cu_seqlens,
                int nseg, const float* shift, const float* scale, int64_t mod_stride, const float* weight,
                const float* bias, float eps, int norm_kind, ditk_stream_t stream);
+
+/*
+ * Several ditk_adaln calls in one launch (1 to 4 jobs of one norm_kind and one
+ * ceil(D / 512)); each job's fields are ditk_adaln's arguments and each row is
+ * computed exactly as ditk_adaln computes it (a job with T == 0 gets no
+ * workgroups).  For the short rows of a step
+ * that would otherwise cost a launch each (SD3.5's 666 text rows beside its
+ * image rows).  No reference counterpart: the reference runs these norms as
+ * separate module calls (sd35_batch.py:656-668,683-685,697,704-706).
+ */
+typedef struct ditk_adaln_job {
+  const void* x;
+  int64_t ldx;
+  void* y;
+  int64_t ldy;
+  const int32_t* cu_seqlens;
+  const float* shift;
+  const float* scale;
+  int64_t mod_stride;
+  const float* weight;
+  const float* bias;
+  int T, D, nseg, norm_kind;
+  float eps;
+} ditk_adaln_job;
+int ditk_adaln_multi(const ditk_adaln_job* jobs, int njobs, ditk_stream_t stream);
 
 /*
  * mod[s, j] = table[j] + proj[s, j] for kd = k*D contiguous fp32 values per segment.
@@ -56,7 +82,7 @@ int ditk_modulation(const float* table, const float* proj, float* mod, int nseg,
  * position; grids: int32 [nseg][3] = (F', H', W') per segment.
  * Replaces: _qk_norm_rope_reference and the fused_qk_norm_rope slot —
  *   transformer_wan.py:24-25,111-115,158-191; SD3.5 per-head norm_q/norm_k —
- *   sd35_batch.py:426-429,439-442.
+ *   sd35_batch.py:428-431,438-441.
  */
 int ditk_qk_norm_rope(void* q, int64_t ldq, void* k, int64_t ldk, int T, int D, int head_dim, const float* wq,
                       const float* wk, float eps, int per_head, const float* rope_cos, const float* rope_sin,
@@ -75,6 +101,30 @@ int ditk_qk_norm_rope_out(const void* q, int64_t ldq, const void* k, int64_t ldk
                           float eps, int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
                           const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
                           ditk_stream_t stream);
+
+/*
+ * Several RoPE-free ditk_qk_norm_rope_out calls in one launch (1 to 4 jobs of
+ * one ceil(D / 512) and one grouping: per_head and head_dim); outputs may equal
+ * the inputs (in place).  Each row is computed exactly as the single call
+ * computes it.  For SD3.5's image and text per-head QK RMSNorms of one block.
+ * No reference counterpart: the reference's norm_q / norm_k / norm_added_q /
+ * norm_added_k are separate module calls (sd35_batch.py:428-431,438-441).
+ */
+typedef struct ditk_qk_norm_job {
+  const void* q;
+  int64_t ldq;
+  const void* k;
+  int64_t ldk;
+  void* q_out;
+  int64_t ldqo;
+  void* k_out;
+  int64_t ldko;
+  const float* wq;
+  const float* wk;
+  int T, D, head_dim, per_head;
+  float eps;
+} ditk_qk_norm_job;
+int ditk_qk_norm_multi(const ditk_qk_norm_job* jobs, int njobs, ditk_stream_t stream);
 
 /*
  * bf16 MFMA GEMM  C = epilogue(A[M,K] W[N,K]^T + bias[N]) with epilogue

@@ -340,6 +340,74 @@ def test_qk_norm_per_head_no_rope():
     assert_close(qd.float().cpu(), rq, cos_min=0.99999, rel_max=5e-3, label="per-head q")
 
 
+# --------------------------------------------------------------------------- multi-job norm launches
+def test_adaln_multi_matches_single_calls():
+    """One launch of several AdaLN jobs writes, per job, bitwise what a single
+    adaln() call writes: modulated LayerNorms over strided [nseg, 6D] modulation
+    views (image, text, the text's (scale, shift) order), a zero-row job between
+    them, an in-place RMSNorm pair; mismatched kinds or widths are refused."""
+    ops = _ops()
+    from ditserve_amd._lib import DitkError
+    D = 1536
+    xi = randn((1000, D), 90, 3.0).to(DEV, torch.bfloat16)
+    xt = randn((333, D), 91, 2.0).to(DEV, torch.bfloat16)
+    modi, modt = randn((2, 6 * D), 92).to(DEV), randn((3, 6 * D), 93).to(DEV)
+    si, st = _seg([0, 500, 1000]), _seg([0, 154, 154, 333])
+    jobs = [dict(x=xi, shift=modi[:, 0:D], scale=modi[:, D:2 * D], segments=si),
+            dict(x=xi[:0], weight=(randn((D,), 94, 0.1) + 1).to(DEV), out=torch.empty_like(xt)[:0]),
+            dict(x=xt, shift=modt[:, D:2 * D], scale=modt[:, 0:D], segments=st, eps=1e-5),
+            dict(x=xi, shift=modi[:, 3 * D:4 * D], scale=modi[:, 4 * D:5 * D], segments=si)]
+    got = ops.adaln_multi(jobs)
+    for j, g in zip(jobs, got):
+        assert torch.equal(g, ops.adaln(**j))
+    assert got[1].shape == (0, D)
+    w = (randn((D,), 95, 0.1) + 1).to(DEV)
+    qi, kt = xi.clone(), xt[:, :1024].clone()
+    with pytest.raises(DitkError):  # ceil(D / 512) differs (3 vs 2)
+        ops.adaln_multi([dict(x=qi, weight=w, kind="rms"), dict(x=kt, weight=w[:1024], kind="rms")])
+    kt = xt.clone()
+    ops.adaln_multi([dict(x=qi, weight=w, kind="rms", out=qi), dict(x=kt, weight=w, kind="rms", out=kt)])
+    assert torch.equal(qi, ops.adaln(xi, weight=w, kind="rms")) and torch.equal(kt, ops.adaln(xt, weight=w, kind="rms"))
+    with pytest.raises(DitkError):  # one launch runs one norm kind
+        ops.adaln_multi([dict(x=xi, weight=w), dict(x=xt, weight=w, kind="rms")])
+    with pytest.raises(DitkError):  # at most four jobs
+        ops.adaln_multi([dict(x=xt)] * 5)
+
+
+@pytest.mark.parametrize("per_head,Dh", [(True, 64), (True, 128), (False, 128)])
+def test_qk_norm_multi_matches_single_calls(per_head, Dh):
+    """One launch of RoPE-free QK-norm jobs (image and text, in place; a third
+    out of place into column slices of another buffer) equals, bitwise, separate
+    qk_norm_rope_() calls; jobs of another grouping are refused."""
+    ops = _ops()
+    from ditserve_amd._lib import DitkError
+    D = 1536
+    qkv_i = randn((1000, 3 * D), 96, 2.0).to(DEV, torch.bfloat16)
+    qkv_t = randn((154, 3 * D), 97, 2.0).to(DEV, torch.bfloat16)
+    n = D if not per_head else Dh
+    wi = [(randn((n,), s, 0.1) + 1).repeat(D // n).to(DEV) for s in (98, 99)]
+    wt = [(randn((n,), s, 0.1) + 1).repeat(D // n).to(DEV) for s in (100, 101)]
+    ref_i, ref_t = qkv_i.clone(), qkv_t.clone()
+    ops.qk_norm_rope_(ref_i[:, :D], ref_i[:, D:2 * D], *wi, Dh, per_head=per_head)
+    ops.qk_norm_rope_(ref_t[:, :D], ref_t[:, D:2 * D], *wt, Dh, per_head=per_head)
+    src = qkv_t.clone()
+    buf = torch.zeros((154, 3 * D), dtype=torch.bfloat16, device=DEV)
+    got = ops.qk_norm_multi([
+        dict(q=qkv_i[:, :D], k=qkv_i[:, D:2 * D], wq=wi[0], wk=wi[1], head_dim=Dh, per_head=per_head),
+        dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh, per_head=per_head),
+        dict(q=src[:, :D], k=src[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh, per_head=per_head,
+             out=(buf[:, :D], buf[:, 2 * D:]))])
+    assert torch.equal(qkv_i, ref_i) and torch.equal(qkv_t, ref_t)
+    assert torch.equal(got[2][0], ref_t[:, :D]) and torch.equal(got[2][1], ref_t[:, D:2 * D])
+    assert torch.equal(buf[:, D:2 * D], torch.zeros_like(buf[:, D:2 * D])) and torch.equal(src[:, 2 * D:],
+                                                                                            qkv_t[:, 2 * D:])
+    other = dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=64 if Dh == 128 else 128,
+                 per_head=True)
+    with pytest.raises(DitkError):
+        ops.qk_norm_multi([dict(q=qkv_i[:, :D], k=qkv_i[:, D:2 * D], wq=wi[0], wk=wi[1], head_dim=Dh,
+                                per_head=per_head), other])
+
+
 # --------------------------------------------------------------------------- attention
 def _attn_case(cu_q, cu_k, H, Dh, seed, scale_in=1.0):
     q = bf(randn((cu_q[-1], H * Dh), seed, scale_in))

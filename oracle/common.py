@@ -37,7 +37,7 @@ def rms_norm(x, weight=None, eps=1e-6):
     """RMSNorm over the last dim: x * rsqrt(mean(x^2) + eps) * weight.
 
     Wan: across all heads (norm_q/norm_k over D), workers/xfuser/model_executor/models/
-    transformers/transformer_wan.py:165-166.  SD3.5: per head (Dh), sd35_batch.py:426-429,439-442.
+    transformers/transformer_wan.py:165-166.  SD3.5: per head (Dh), sd35_batch.py:428-431,438-441.
     """
     y = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
     if weight is not None:

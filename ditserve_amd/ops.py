@@ -210,8 +210,12 @@ def adaln(x, shift=None, scale=None, segments=None, weight=None, bias=None, eps=
 def adaln_multi(jobs):
     """Several adaln() calls (dicts of its keyword arguments, x required) in one
     launch: 1 to 4 jobs of one kind and one ceil(D / 512).  Returns the outputs;
-    each is bitwise what adaln() returns for its job."""
+    each is bitwise what adaln() returns for its job.  The jobs run concurrently:
+    a job's output may be its own x (in place) but may not overlap another
+    job's tensors."""
     built = [_adaln_job(**j) for j in jobs]
+    _disjoint_jobs("adaln_multi", [((b[0],), tuple(j.get(k) for k in ("x", "shift", "scale", "weight", "bias")))
+                                   for j, b in zip(jobs, built)])
     arr = (_lib.AdalnJob * len(built))(*[b[1] for b in built])
     _lib.call("ditk_adaln_multi", arr, len(built), _stream())
     return [b[0] for b in built]
@@ -224,6 +228,9 @@ def _adaln_job(x, shift=None, scale=None, segments=None, weight=None, bias=None,
     ldx = _rows(x, "x")
     if out is None:
         out = torch.empty((T, D), dtype=_BF16, device=x.device)
+    _check(out, "out", _BF16, 2)
+    if out.shape != (T, D):
+        raise ValueError(f"out must be [{T}, {D}], got {tuple(out.shape)}")
     ldy = _rows(out, "out")
     mod_stride = 0
     cu = None
@@ -305,7 +312,9 @@ def qk_norm_multi(jobs):
     """Several RoPE-free qk_norm_rope_() calls in one launch: jobs are dicts with
     q, k, wq, wk, head_dim and optionally eps, per_head, out (1 to 4 jobs of one
     ceil(D / 512), head_dim and per_head).  Each job's result is bitwise what
-    qk_norm_rope_() gives it; returns the (q, k) pairs written."""
+    qk_norm_rope_() gives it; returns the (q, k) pairs written.  The jobs run
+    concurrently: a job may write in place, but its outputs may not overlap
+    another job's tensors."""
     built, ret = [], []
     for j in jobs:
         q, k, wq, wk = j["q"], j["k"], j["wq"], j["wk"]
@@ -327,6 +336,7 @@ def qk_norm_multi(jobs):
                                     _ptr(ko), _rows(ko, "k_out"), _ptr(wq), _ptr(wk), T, D, int(j["head_dim"]),
                                     int(bool(j.get("per_head", False))), float(j.get("eps", 1e-6))))
         ret.append((qo, ko))
+    _disjoint_jobs("qk_norm_multi", [(r, (j["q"], j["k"], j["wq"], j["wk"])) for j, r in zip(jobs, ret)])
     arr = (_lib.QkNormJob * len(built))(*built)
     _lib.call("ditk_qk_norm_multi", arr, len(built), _stream())
     return ret
@@ -444,6 +454,20 @@ def _overlap(a, b):
     return a0 < b1 and b0 < a1
 
 
+def _disjoint_jobs(fn, jobs_io):
+    """jobs_io: per job (outputs, operands).  The jobs of one launch run
+    concurrently, so no job's output may overlap another job's operands or
+    outputs (its own operands it may overwrite in place)."""
+    for i, (outs, _) in enumerate(jobs_io):
+        for j, (outs_j, ops_j) in enumerate(jobs_io):
+            if i == j:
+                continue
+            for o in outs:
+                for t in (*outs_j, *ops_j):
+                    if t is not None and _overlap(o, t):
+                        raise ValueError(f"{fn}: job {i}'s output overlaps a tensor of job {j}")
+
+
 def linear_pair(p0, p1, epilogue="bias"):
     """Two linear() products of the same N, K and epilogue (e.g. an SD3.5 block's
     image and text projections), in one launch when their tiles fit the larger
@@ -481,9 +505,16 @@ def transpose_v(v, heads, head_dim, segments, out=None):
     """V [Tk, heads*head_dim] -> Vt [heads, head_dim, cols] with per-segment 64-aligned columns."""
     _check(v, "v", _BF16, 2)
     ldv = _rows(v, "v")
+    if v.shape[1] != heads * head_dim:
+        raise ValueError(f"v must have heads * head_dim = {heads * head_dim} columns, got {v.shape[1]}")
+    if segments.total != v.shape[0]:
+        raise ValueError(f"segments cover {segments.total} keys, v has {v.shape[0]} rows")
     cols = vt_columns(v.shape[0], segments.nseg)
     if out is None:
         out = torch.empty((heads, head_dim, cols), dtype=_BF16, device=v.device)
+    _check(out, "out", _BF16, 3)
+    if out.shape != (heads, head_dim, cols) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{heads}, {head_dim}, {cols}] buffer")
     _lib.call("ditk_transpose_v", _ptr(v), ldv, _ptr(out), cols, v.shape[0], heads, head_dim,
               _ptr(segments.dev), segments.nseg, _stream())
     return out
@@ -524,6 +555,9 @@ def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None
     Tq = q.shape[0]
     if out is None:
         out = torch.empty((Tq, width), dtype=_BF16, device=q.device)
+    _check(out, "out", _BF16, 2)
+    if out.shape != (Tq, width):
+        raise ValueError(f"out must be [{Tq}, {width}], got {tuple(out.shape)}")
     ldo = _rows(out, "out")
     lse = torch.empty((heads, Tq), dtype=torch.float32, device=q.device) if return_lse else None
     if q_prescaled:
@@ -614,13 +648,32 @@ def solver_step(x, cond, coef, uncond=None, x_last=None, m_prev=None, m_prev2=No
 
 def joint_gather(img, txt, seg_img, seg_txt, out=None):
     """Interleave per segment: [img rows of m, txt rows of m] -> joint [Ti+Tt, W]."""
-    total = seg_img.total + seg_txt.total
-    width = img.shape[1]
+    total, width = _joint_copy_check(img, txt, seg_img, seg_txt)
     if out is None:
         out = torch.empty((total, width), dtype=_BF16, device=img.device)
+    _joint_rows_check(out, "out", total, width)
     _lib.call("ditk_joint_copy", _ptr(img), img.stride(0), _ptr(txt), txt.stride(0), _ptr(out), out.stride(0),
               _ptr(seg_img.dev), _ptr(seg_txt.dev), seg_img.nseg, total, width, 0, _stream())
     return out
+
+
+def _joint_rows_check(t, name, rows, width):
+    _check(t, name, _BF16, 2)
+    _rows(t, name)
+    if t.shape != (rows, width):
+        raise ValueError(f"{name} must be [{rows}, {width}], got {tuple(t.shape)}")
+
+
+def _joint_copy_check(img, txt, seg_img, seg_txt):
+    """Operands of a joint gather / scatter: image rows [seg_img.total, W] and text
+    rows [seg_txt.total, W], both bf16 row views; returns (joint rows, W)."""
+    if seg_img.nseg != seg_txt.nseg:
+        raise ValueError("image and text segment tables must have the same number of segments")
+    _check(img, "img", _BF16, 2)
+    width = img.shape[1]
+    _joint_rows_check(img, "img", seg_img.total, width)
+    _joint_rows_check(txt, "txt", seg_txt.total, width)
+    return seg_img.total + seg_txt.total, width
 
 
 def _joint_tables(seg_img, seg_txt, seg_joint):
@@ -686,7 +739,8 @@ def joint_attention_q_prescaled(q_img, q_txt, k_img, k_txt, vt, seg_img, seg_txt
 
 def joint_scatter(joint, img, txt, seg_img, seg_txt):
     """Inverse of joint_gather: joint rows back into img / txt buffers."""
-    total = seg_img.total + seg_txt.total
+    total, width = _joint_copy_check(img, txt, seg_img, seg_txt)
+    _joint_rows_check(joint, "joint", total, width)
     _lib.call("ditk_joint_copy", _ptr(img), img.stride(0), _ptr(txt), txt.stride(0), _ptr(joint),
               joint.stride(0), _ptr(seg_img.dev), _ptr(seg_txt.dev), seg_img.nseg, total, joint.shape[1], 1,
               _stream())

@@ -47,9 +47,10 @@ int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int T, int D, c
  * Several ditk_adaln calls in one launch (1 to 4 jobs of one norm_kind and one
  * ceil(D / 512)); each job's fields are ditk_adaln's arguments and each row is
  * computed exactly as ditk_adaln computes it (a job with T == 0 gets no
- * workgroups).  For the short rows of a step
- * that would otherwise cost a launch each (SD3.5's 666 text rows beside its
- * image rows).  No reference counterpart: the reference runs these norms as
+ * workgroups).  The jobs run concurrently: a job's output may be its own x
+ * (in place) but must not overlap another job's tensors.  For the short rows
+ * of a step that would otherwise cost a launch each (SD3.5's 666 text rows
+ * beside its image rows).  No reference counterpart: the reference runs these norms as
  * separate module calls (sd35_batch.py:656-668,683-685,697,704-706).
  */
 typedef struct ditk_adaln_job {
@@ -105,8 +106,9 @@ int ditk_qk_norm_rope_out(const void* q, int64_t ldq, const void* k, int64_t ldk
 /*
  * Several RoPE-free ditk_qk_norm_rope_out calls in one launch (1 to 4 jobs of
  * one ceil(D / 512) and one grouping: per_head and head_dim); outputs may equal
- * the inputs (in place).  Each row is computed exactly as the single call
- * computes it.  For SD3.5's image and text per-head QK RMSNorms of one block.
+ * the job's own inputs (in place) but must not overlap another job's tensors.
+ * Each row is computed exactly as the single call computes it.  For SD3.5's
+ * image and text per-head QK RMSNorms of one block.
  * No reference counterpart: the reference's norm_q / norm_k / norm_added_q /
  * norm_added_k are separate module calls (sd35_batch.py:428-431,438-441).
  */

@@ -372,6 +372,14 @@ def test_adaln_multi_matches_single_calls():
         ops.adaln_multi([dict(x=xi, weight=w), dict(x=xt, weight=w, kind="rms")])
     with pytest.raises(DitkError):  # at most four jobs
         ops.adaln_multi([dict(x=xt)] * 5)
+    a, b = xt.clone(), xt.clone()
+    with pytest.raises(ValueError):  # a job may not write another job's input (they run concurrently)
+        ops.adaln_multi([dict(x=a, weight=w, kind="rms", out=b), dict(x=b, weight=w, kind="rms")])
+    with pytest.raises(ValueError):  # nor share an output with it
+        ops.adaln_multi([dict(x=a, weight=w, kind="rms", out=b), dict(x=xt, weight=w, kind="rms", out=b)])
+    with pytest.raises(ValueError):  # an output of another row count
+        ops.adaln(xi, weight=w, kind="rms", out=a)
+    assert torch.equal(a, xt) and torch.equal(b, xt)
 
 
 @pytest.mark.parametrize("per_head,Dh", [(True, 64), (True, 128), (False, 128)])
@@ -406,6 +414,10 @@ def test_qk_norm_multi_matches_single_calls(per_head, Dh):
     with pytest.raises(DitkError):
         ops.qk_norm_multi([dict(q=qkv_i[:, :D], k=qkv_i[:, D:2 * D], wq=wi[0], wk=wi[1], head_dim=Dh,
                                 per_head=per_head), other])
+    with pytest.raises(ValueError):  # one job's output over another job's q
+        ops.qk_norm_multi([dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh,
+                                per_head=per_head, out=(src[:, :D], src[:, 2 * D:])),
+                           dict(q=src[:, :D], k=src[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh, per_head=per_head)])
 
 
 # --------------------------------------------------------------------------- attention
@@ -767,3 +779,24 @@ def test_invalid_arguments_raise_before_launch():
     with pytest.raises((ValueError, DitkError)):  # output rows not 16-byte aligned (4-element column offset)
         ops.qk_norm_rope_(q, q.clone(), w, w, 64, out=(big[:, 4:132], q.clone()))
     assert torch.equal(q, torch.zeros_like(q))
+    # caller-supplied outputs and operands of the wrong size are refused before any launch
+    v = torch.zeros((10, 256), dtype=torch.bfloat16, device=DEV)
+    seg = _seg([0, 4, 10])
+    with pytest.raises(ValueError):  # v narrower than heads * head_dim
+        ops.transpose_v(v, 3, 128, seg)
+    with pytest.raises(ValueError):  # Vt buffer too small
+        ops.transpose_v(v, 2, 128, seg, out=torch.empty((2, 128, 64), dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):  # table of another token count
+        ops.transpose_v(v, 2, 128, _seg([0, 4, 9]))
+    with pytest.raises(ValueError):  # attention output of too few rows
+        ops.flash_attn_varlen(v, v, v, seg, seg, 2, 128, out=torch.empty((9, 256), dtype=torch.bfloat16, device=DEV))
+    img, txt = torch.zeros((10, 64), dtype=torch.bfloat16, device=DEV), torch.zeros((6, 64), dtype=torch.bfloat16,
+                                                                                   device=DEV)
+    si, st = _seg([0, 4, 10]), _seg([0, 3, 6])
+    with pytest.raises(ValueError):  # text rows of another width
+        ops.joint_gather(img, torch.zeros((6, 128), dtype=torch.bfloat16, device=DEV), si, st)
+    with pytest.raises(ValueError):  # joint buffer of too few rows
+        ops.joint_gather(img, txt, si, st, out=torch.empty((15, 64), dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):  # scatter source of too few rows
+        ops.joint_scatter(torch.empty((15, 64), dtype=torch.bfloat16, device=DEV), img, txt, si, st)
+    torch.cuda.synchronize()

@@ -594,6 +594,9 @@ def unpatchify(x, grid, patch, channels):
     ldx = x.stride(0)
     Fp, Hp, Wp = grid
     pt, ph, pw = patch
+    if x.shape != (Fp * Hp * Wp, pt * ph * pw * channels) or x.stride(1) != 1:
+        raise ValueError(f"x must be [{Fp * Hp * Wp}, {pt * ph * pw * channels}] with unit column stride, "
+                         f"got {tuple(x.shape)}")
     out = torch.empty((channels, Fp * pt, Hp * ph, Wp * pw), dtype=torch.float32, device=x.device)
     _lib.call("ditk_unpatchify", _ptr(x), ldx, _ptr(out), channels, Fp, Hp, Wp, pt, ph, pw, _stream())
     return out
@@ -612,7 +615,9 @@ def cfg_combine(cond, uncond, guidance):
     """uncond + g * (cond - uncond), fp32."""
     _check(cond, "cond", torch.float32)
     _check(uncond, "uncond", torch.float32)
-    out = torch.empty_like(cond)
+    if cond.shape != uncond.shape:
+        raise ValueError(f"cond and uncond shapes differ: {tuple(cond.shape)} vs {tuple(uncond.shape)}")
+    out = torch.empty_like(cond, memory_format=torch.contiguous_format)
     _lib.call("ditk_cfg_combine", _ptr(cond.contiguous()), _ptr(uncond.contiguous()), _ptr(out), cond.numel(),
               float(guidance), _stream())
     return out
@@ -728,6 +733,10 @@ def joint_attention_q_prescaled(q_img, q_txt, k_img, k_txt, vt, seg_img, seg_txt
         out_img = torch.empty((seg_img.total, width), dtype=_BF16, device=q_img.device)
     if out_txt is None:
         out_txt = torch.empty((seg_txt.total, width), dtype=_BF16, device=q_img.device)
+    for t, n, rows in ((out_img, "out_img", seg_img.total), (out_txt, "out_txt", seg_txt.total)):
+        _check(t, n, _BF16, 2)
+        if t.shape != (rows, width):
+            raise ValueError(f"{n} must be [{rows}, {width}], got {tuple(t.shape)}")
     if _rows(out_img, "out_img") != _rows(out_txt, "out_txt"):
         raise ValueError("out_img and out_txt must share a row stride")
     _lib.call("ditk_joint_attn_q_prescaled", _ptr(q_img), _ptr(q_txt), _rows(q_img, "q_img"), _ptr(k_img),

@@ -799,4 +799,11 @@ def test_invalid_arguments_raise_before_launch():
         ops.joint_gather(img, txt, si, st, out=torch.empty((15, 64), dtype=torch.bfloat16, device=DEV))
     with pytest.raises(ValueError):  # scatter source of too few rows
         ops.joint_scatter(torch.empty((15, 64), dtype=torch.bfloat16, device=DEV), img, txt, si, st)
+    with pytest.raises(ValueError):  # joint attention output of too few rows
+        vtj = torch.zeros((1, 64, ops.vt_columns(16, 2)), dtype=torch.bfloat16, device=DEV)
+        ops.joint_attention_q_prescaled(img, txt, img, txt, vtj, si, st, _seg([0, 7, 16]), 1, 64, out_img=img[:9])
+    with pytest.raises(ValueError):  # rows that are not the grid's tokens
+        ops.unpatchify(torch.zeros((11, 64), dtype=torch.bfloat16, device=DEV), (1, 2, 5), (1, 2, 2), 16)
+    with pytest.raises(ValueError):  # CFG branches of different sizes
+        ops.cfg_combine(torch.zeros(8, device=DEV), torch.zeros(6, device=DEV), 5.0)
     torch.cuda.synchronize()

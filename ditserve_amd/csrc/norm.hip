@@ -17,7 +17,10 @@ constexpr int kMaxChunks = 8;     // 16-byte chunks per lane -> D <= 64*8*8 = 40
 // AdaLN:  y = norm(x) [* w + b] [* (1 + scale[seg]) + shift[seg]]
 //   norm = LayerNorm (kind 0) or RMSNorm (kind 1), eps inside the rsqrt.
 // ---------------------------------------------------------------------------
-template <int KIND, int NC>
+// AFF: an unmodulated row with affine weight and/or bias, whose vectors are
+// then loaded before the reductions like the modulation (a variant of its own,
+// so that the modulated kernels keep their register allocation).
+template <int KIND, int NC, bool AFF = false>
 __device__ __forceinline__ void adaln_row(
     const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int row, int D,
     const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
@@ -28,7 +31,8 @@ __device__ __forceinline__ void adaln_row(
   const bf16_t* xr = x + (int64_t)row * ldx;
   // Every load of the row is issued before the reductions: the row itself
   // (NC 16-byte chunks per lane, kept packed), then its segment's scale and
-  // shift (L2-resident), so the latencies overlap.
+  // shift or, unmodulated, the affine weight and bias (L2-resident), so the
+  // latencies overlap.
   u32x4_t raw[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -36,7 +40,20 @@ __device__ __forceinline__ void adaln_row(
     raw[i] = c < nchunk ? *reinterpret_cast<const u32x4_t*>(xr + c * 8) : u32x4_t{0, 0, 0, 0};
   }
   f32x4_t sc4[NC][2], sh4[NC][2];
-  const bool mod = shift != nullptr;
+  const bool mod = !AFF && shift != nullptr;
+  // AFF rows hold the affine vectors in the modulation's registers: sc4 = w, sh4 = b
+  constexpr bool aff_pre = AFF;
+  if (aff_pre) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(i * 64 + lane, nchunk - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        sc4[i][h] = w != nullptr ? *reinterpret_cast<const f32x4_t*>(w + c * 8 + 4 * h) : f32x4_t{1.f, 1.f, 1.f, 1.f};
+        sh4[i][h] = b != nullptr ? *reinterpret_cast<const f32x4_t*>(b + c * 8 + 4 * h) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
   if (mod) {
     const int seg = find_segment(cu, nseg, row);
     const float* sh = shift + (int64_t)seg * mod_stride;
@@ -96,12 +113,24 @@ __device__ __forceinline__ void adaln_row(
       unpack8(raw[i], o);
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = (o[j] - mean) * rstd;
-      if (w != nullptr) {
+      if (aff_pre) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (w != nullptr) {
+            o[j] *= sc4[i][0][j];
+            o[j + 4] *= sc4[i][1][j];
+          }
+          if (b != nullptr) {
+            o[j] += sh4[i][0][j];
+            o[j + 4] += sh4[i][1][j];
+          }
+        }
+      } else if (w != nullptr) {
         load8(w + c * 8, t);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] *= t[j];
       }
-      if (b != nullptr) {
+      if (!aff_pre && b != nullptr) {
         load8(b + c * 8, t);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] += t[j];
@@ -118,7 +147,7 @@ __device__ __forceinline__ void adaln_row(
   }
 }
 
-template <int KIND, int NC>
+template <int KIND, int NC, bool AFF>
 __global__ __launch_bounds__(256) void adaln_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, bf16_t* __restrict__ y, int64_t ldy, int T, int D,
     const int32_t* __restrict__ cu, int nseg, const float* __restrict__ shift,
@@ -126,7 +155,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(
     const float* __restrict__ b, float eps) {
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= T) return;
-  adaln_row<KIND, NC>(x, ldx, y, ldy, row, D, cu, nseg, shift, scale, mod_stride, w, b, eps);
+  adaln_row<KIND, NC, AFF>(x, ldx, y, ldy, row, D, cu, nseg, shift, scale, mod_stride, w, b, eps);
 }
 
 // Several AdaLN jobs of one norm kind and chunk count in one launch: job j owns
@@ -153,14 +182,14 @@ struct AdalnJobs {
   int njobs;
 };
 
-template <int KIND, int NC>
+template <int KIND, int NC, bool AFF>
 __global__ __launch_bounds__(256) void adaln_multi_kernel(AdalnJobs jobs) {
   int j = 0;
   while (j + 1 < jobs.njobs && (int)blockIdx.x >= jobs.block0[j + 1]) ++j;
   const AdalnJob& a = jobs.job[j];
   const int row = ((int)blockIdx.x - jobs.block0[j]) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= a.T) return;
-  adaln_row<KIND, NC>(a.x, a.ldx, a.y, a.ldy, row, a.D, a.cu, a.nseg, a.shift, a.scale, a.mod_stride, a.w, a.b,
+  adaln_row<KIND, NC, AFF>(a.x, a.ldx, a.y, a.ldy, row, a.D, a.cu, a.nseg, a.shift, a.scale, a.mod_stride, a.w, a.b,
                       a.eps);
 }
 
@@ -391,9 +420,10 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
   if (T == 0) return 0;
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
-#define DITK_ADALN(K, NCV)                                                                            \
-  adaln_kernel<K, NCV><<<grid, 256, 0, stream>>>((const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens, \
-                                                 nseg, shift, scale, mod_stride, weight, bias, eps)
+  const bool aff = shift == nullptr && (weight != nullptr || bias != nullptr);
+#define DITK_ADALN(K, NCV)                                                                                     \
+  (aff ? adaln_kernel<K, NCV, true> : adaln_kernel<K, NCV, false>)<<<grid, 256, 0, stream>>>(                  \
+      (const bf16_t*)x, ldx, (bf16_t*)y, ldy, T, D, cu_seqlens, nseg, shift, scale, mod_stride, weight, bias, eps)
 #define DITK_ADALN_NC(K)              \
   switch (nc) {                       \
     case 1: DITK_ADALN(K, 1); break;  \
@@ -420,9 +450,11 @@ DITK_EXPORT int ditk_adaln_multi(const ditk_adaln_job* jobs, int njobs, hipStrea
   AdalnJobs a = {};
   a.njobs = njobs;
   int nc = 0, kind = 0;
+  bool aff = true;  // every job unmodulated with affine vectors
   int64_t blocks = 0;
   for (int j = 0; j < njobs; ++j) {
     const ditk_adaln_job& p = jobs[j];
+    aff = aff && p.shift == nullptr && (p.weight != nullptr || p.bias != nullptr);
     const int rc = adaln_check(p.x, p.ldx, p.y, p.ldy, p.T, p.D, p.cu_seqlens, p.nseg, p.shift, p.scale,
                                p.mod_stride, p.weight, p.bias, p.norm_kind);
     if (rc) return rc;
@@ -440,7 +472,8 @@ DITK_EXPORT int ditk_adaln_multi(const ditk_adaln_job* jobs, int njobs, hipStrea
   a.block0[njobs] = (int)blocks;
   if (blocks == 0) return 0;
   const dim3 grid((unsigned)blocks);
-#define DITK_ADALN_M(K, NCV) adaln_multi_kernel<K, NCV><<<grid, 256, 0, stream>>>(a)
+#define DITK_ADALN_M(K, NCV) \
+  (aff ? adaln_multi_kernel<K, NCV, true> : adaln_multi_kernel<K, NCV, false>)<<<grid, 256, 0, stream>>>(a)
 #define DITK_ADALN_M_NC(K)              \
   switch (nc) {                         \
     case 1: DITK_ADALN_M(K, 1); break;  \

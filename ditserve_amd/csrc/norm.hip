@@ -11,7 +11,7 @@
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
-constexpr int kMaxChunks = 8;     // 16-byte chunks per lane -> D <= 64*8*8 = 4096
+constexpr int kMaxChunks = 12;    // 16-byte chunks per lane -> D <= 64*8*12 = 6144
 
 // ---------------------------------------------------------------------------
 // AdaLN:  y = norm(x) [* w + b] [* (1 + scale[seg]) + shift[seg]]
@@ -433,7 +433,10 @@ DITK_EXPORT int ditk_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int
     case 5: DITK_ADALN(K, 5); break;  \
     case 6: DITK_ADALN(K, 6); break;  \
     case 7: DITK_ADALN(K, 7); break;  \
-    default: DITK_ADALN(K, 8); break; \
+    case 8: DITK_ADALN(K, 8); break;   \
+    case 9:                         \
+    case 10: DITK_ADALN(K, 10); break; \
+    default: DITK_ADALN(K, 12); break; \
   }
   if (norm_kind == 0) {
     DITK_ADALN_NC(0)
@@ -483,7 +486,10 @@ DITK_EXPORT int ditk_adaln_multi(const ditk_adaln_job* jobs, int njobs, hipStrea
     case 5: DITK_ADALN_M(K, 5); break;  \
     case 6: DITK_ADALN_M(K, 6); break;  \
     case 7: DITK_ADALN_M(K, 7); break;  \
-    default: DITK_ADALN_M(K, 8); break; \
+    case 8: DITK_ADALN_M(K, 8); break;   \
+    case 9:                         \
+    case 10: DITK_ADALN_M(K, 10); break; \
+    default: DITK_ADALN_M(K, 12); break; \
   }
   if (kind == 0) {
     DITK_ADALN_M_NC(0)
@@ -554,7 +560,10 @@ int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, 
     case 5: DITK_QKN(G, 5); break;  \
     case 6: DITK_QKN(G, 6); break;  \
     case 7: DITK_QKN(G, 7); break;  \
-    default: DITK_QKN(G, 8); break; \
+    case 8: DITK_QKN(G, 8); break;   \
+    case 9:                         \
+    case 10: DITK_QKN(G, 10); break; \
+    default: DITK_QKN(G, 12); break; \
   }
   if (!per_head) {
     DITK_QKN_NC(64)
@@ -605,7 +614,10 @@ DITK_EXPORT int ditk_qk_norm_multi(const ditk_qk_norm_job* jobs, int njobs, hipS
     case 5: DITK_QKM(G, 5); break;  \
     case 6: DITK_QKM(G, 6); break;  \
     case 7: DITK_QKM(G, 7); break;  \
-    default: DITK_QKM(G, 8); break; \
+    case 8: DITK_QKM(G, 8); break;   \
+    case 9:                         \
+    case 10: DITK_QKM(G, 10); break; \
+    default: DITK_QKM(G, 12); break; \
   }
   if (group == 64) {
     DITK_QKM_NC(64)

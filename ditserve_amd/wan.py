@@ -75,6 +75,8 @@ class WanConfig:
 
 WAN21_T2V_1_3B = WanConfig()
 WAN22_TI2V_5B = WanConfig(dim=3072, heads=24, ffn=14336, in_ch=48, out_ch=48)
+# the published Wan2.1-T2V-14B transformer config (workers/ditserve/evaluation/cost_profile.py:19-20)
+WAN21_T2V_14B = WanConfig(dim=5120, heads=40, ffn=13824, layers=40)
 
 
 # ---------------------------------------------------------------------------

@@ -37,8 +37,13 @@ def pos_embed_table(dim, max_size=384, base_size=64, interpolation_scale=1.0):
     return torch.cat([sincos_1d(dim // 2, gw), sincos_1d(dim // 2, gh)], dim=1).float()
 
 
-def cropped_pos_embed(table, hp, wp, max_size=384):
-    """Centre crop of the table for an hp x wp patch grid -> [hp*wp, dim]."""
+def cropped_pos_embed(table, hp, wp):
+    """Centre crop of a [max_size^2, dim] table for an hp x wp patch grid -> [hp*wp, dim]
+    (max_size = pos_embed_max_size, read off the table: 384 for SD3.5-Medium, 192 for
+    -Large)."""
+    max_size = int(round(table.shape[0] ** 0.5))
+    if max_size * max_size != table.shape[0] or hp > max_size or wp > max_size:
+        raise ValueError(f"a {hp} x {wp} grid does not crop from a {table.shape[0]}-row table")
     top, left = (max_size - hp) // 2, (max_size - wp) // 2
     return table.view(max_size, max_size, -1)[top:top + hp, left:left + wp].reshape(hp * wp, -1)
 

@@ -250,7 +250,7 @@ def test_gemm_stage_depths_agree():
 
 
 # --------------------------------------------------------------------------- AdaLN
-@pytest.mark.parametrize("D", [1536, 3072, 64])
+@pytest.mark.parametrize("D", [1536, 3072, 64, 5120, 6144])  # 5120: Wan2.1-14B; 6144: the widest row
 def test_adaln_modulated_layernorm(D):
     ops = _ops()
     cu = [0, 37, 300, 301, 512]
@@ -278,10 +278,12 @@ def test_adaln_affine_and_rms():
 
 
 # --------------------------------------------------------------------------- QK norm + RoPE
-def test_qk_norm_rope_matches_oracle():
+@pytest.mark.parametrize("D", [1536, 5120])  # Wan2.1-1.3B and -14B (40 heads)
+def test_qk_norm_rope_matches_oracle(D):
     ops = _ops()
     from ditserve_amd.wan import rope_axis_pairs, rope_tables
-    D, H, Dh = 1536, 12, 128
+    Dh = 128
+    H = D // Dh
     grids = [(3, 5, 7), (2, 4, 6), (1, 1, 1)]
     counts = [f * h * w for f, h, w in grids]
     cu = [0, counts[0], counts[0] + counts[1], sum(counts)]
@@ -329,9 +331,10 @@ def test_qk_norm_rope_out_of_place_bitwise():
     assert torch.equal(k, randn((T, D), 61, 2.0).to(DEV, torch.bfloat16))
 
 
-def test_qk_norm_per_head_no_rope():
+@pytest.mark.parametrize("D", [1536, 2432])  # SD3.5-Medium and -Large (38 heads of 64)
+def test_qk_norm_per_head_no_rope(D):
     ops = _ops()
-    T, D, Dh = 100, 1536, 64
+    T, Dh = 100, 64
     q, k = bf(randn((T, D), 22)), bf(randn((T, D), 23))
     wq, wk = bf(randn((Dh,), 24, 0.1) + 1), bf(randn((Dh,), 25, 0.1) + 1)
     qd, kd = q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16)
@@ -806,4 +809,6 @@ def test_invalid_arguments_raise_before_launch():
         ops.unpatchify(torch.zeros((11, 64), dtype=torch.bfloat16, device=DEV), (1, 2, 5), (1, 2, 2), 16)
     with pytest.raises(ValueError):  # CFG branches of different sizes
         ops.cfg_combine(torch.zeros(8, device=DEV), torch.zeros(6, device=DEV), 5.0)
+    with pytest.raises(DitkError):  # rows wider than the row kernels hold in registers (6144)
+        ops.adaln(torch.zeros((4, 6152), dtype=torch.bfloat16, device=DEV))
     torch.cuda.synchronize()

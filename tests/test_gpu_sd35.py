@@ -48,6 +48,19 @@ def test_sd35_small_depth_packed_matches_oracle_and_solo():
         assert torch.equal(outs[m], solo[0]), f"request {m}: packed != solo"
 
 
+def test_sd35_large_shaped_blocks_match_oracle():
+    """The SD3.5-Large block shape (38 heads of 64, hidden 2432, FFN 9728, no dual
+    attention, position table 192), two blocks (the second context_pre_only) at 256^2."""
+    sd35 = _sd()
+    cfg = sd35.SD35Config(dim=2432, heads=38, layers=2, dual_layers=(), ffn=9728, pos_max=192)
+    sd = sd35.random_state_dict(cfg, seed=3)
+    model = sd35.SD35Transformer(cfg, sd, DEV)
+    lat, txt, pooled = _inputs(20, 256)
+    outs, _ = model.forward_packed([lat.to(DEV)], [400.0], [txt.to(DEV)], [pooled.to(DEV)])
+    ref = osd.forward(sd, cfg.oracle_dict(), bf(lat), 400.0, bf(txt), bf(pooled))
+    assert_close(outs[0].cpu(), ref, 0.999, 2e-2, "sd35-large-shaped 2 blocks")
+
+
 def test_sd35_medium_24_blocks_512px_matches_oracle():
     """Full SD3.5-Medium architecture (24 joint blocks, 13 dual) at 512^2 (1024 image tokens)."""
     sd35 = _sd()

@@ -6,9 +6,10 @@
 * Wan2.2-TI2V-5B architecture, 30 blocks, latent 48x31x44x80 (704x1280x121 frames):
   the CFG pair packed as 2 x 27280 tokens (text valid 150 / 0, t = 700) gives finite
   outputs, each segment bitwise equal to its solo forward.
-* One Wan2.2-5B block at 4096 tokens and one Wan2.1 block at the full 21x30x52
-  grid (32760 tokens) against the CPU fp32 oracle (torch's CPU flash SDPA for the
-  32760-token self-attention), cos >= 0.999 and relative L2 <= 1e-2.
+* One Wan2.2-5B block at 4096 tokens, one Wan2.1-14B block at 128 tokens and one
+  Wan2.1 block at the full 21x30x52 grid (32760 tokens) against the CPU fp32
+  oracle (torch's CPU flash SDPA for the 32760-token self-attention), cos >= 0.999
+  and relative L2 <= 1e-2.
 """
 import pytest
 import torch
@@ -80,6 +81,15 @@ def test_wan22_5b_block_4096_tokens_matches_oracle():
     from ditserve_amd.wan import WanConfig
     cfg = WanConfig(dim=3072, heads=24, ffn=14336, in_ch=48, out_ch=48, layers=1)
     _block_vs_oracle(cfg, (4, 32, 32), 150, 700.0, 60, oc.sdpa, "wan2.2-5b block, 4096 tokens")
+
+
+def test_wan21_14b_block_matches_oracle():
+    """One block of the Wan2.1-T2V-14B architecture (D = 5120, 40 heads, FFN 13824:
+    the widest rows the row kernels take, 10 chunks per lane) over 128 tokens."""
+    from ditserve_amd.wan import WAN21_T2V_14B
+    import dataclasses
+    cfg = dataclasses.replace(WAN21_T2V_14B, layers=1)
+    _block_vs_oracle(cfg, (2, 8, 8), 77, 500.0, 80, oc.sdpa, "wan2.1-14b block, 128 tokens")
 
 
 def test_wan21_block_full_grid_32760_tokens_matches_oracle():

@@ -228,6 +228,16 @@ def test_sd35_pos_embed_closed_form_and_crop():
     from ditserve_amd.sd35 import SD35Config, pos_embed_crop
     prod = pos_embed_crop(SD35Config(dim=64), 64, 64, "cpu")
     assert torch.allclose(prod, crop, atol=1e-6)
+    # a 192-wide table (SD3.5-Large's pos_embed_max_size): the crop of a 16 x 16 grid
+    # starts at row = column = 88, coordinates i * 64 / 192
+    t192 = osd.pos_embed_table(64, max_size=192, base_size=64)
+    c192 = osd.cropped_pos_embed(t192, 16, 16)
+    assert c192.shape == (256, 64)
+    r, c = 88 + 3, 88 + 5
+    w = 1.0 / 10000 ** (2 / 16.0)
+    assert abs(float(c192[3 * 16 + 5, 2]) - math.sin((c * 64 / 192) * w)) < 1e-6
+    assert abs(float(c192[3 * 16 + 5, 32 + 2]) - math.sin((r * 64 / 192) * w)) < 1e-6
+    assert torch.allclose(pos_embed_crop(SD35Config(dim=64, pos_max=192), 16, 16, "cpu"), c192, atol=1e-6)
 
 
 def test_sd35_adaln_chunk_orders():

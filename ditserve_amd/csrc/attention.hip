@@ -99,7 +99,7 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
 // placed by hand: O^T and Q in AGPRs, S^T and P in VGPRs, so that the whole
 // working set stays in registers.
 #define DITK_ATTN_ASM_OPERANDS                                                                                      \
-  [qbase] "s"(su64(qbase)), [qoff0] "v"(qoff0), [qoff1] "v"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),            \
+  [qbase_lo] "s"(su((uint32_t)qbase)), [qbase_hi] "s"(su((uint32_t)(qbase >> 32))), [kdma_lo] "s"(su((uint32_t)kdma)), \
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
@@ -110,11 +110,11 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
       [koff0] "v"(koff[0]), [koff1] "v"(koff[1]), [koff2] "v"(koff[2]), [koff3] "v"(koff[3]),                     \
       [koffl0] "v"(koffl[0]), [koffl1] "v"(koffl[1]), [koffl2] "v"(koffl[2]), [koffl3] "v"(koffl[3]),             \
       [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
-      [xaddr] "v"(xaddr), [hh8] "v"(hh8), [lane] "v"(lanev), [qrow0] "v"(qrow0), [qrow1] "v"(qrow1)
+      [lane] "v"(lanev), [qrow0] "v"(qrow0), [qrow1] "v"(qrow1)
 // Pre-scaled q: the body's -m blocks take 32 more VGPRs, so the per-lane values
 // it reads only outside the key loop arrive in AGPRs
 #define DITK_ATTN_ASM_OPERANDS_PRE                                                                                  \
-  [qbase] "s"(su64(qbase)), [qoff0] "a"(qoff0), [qoff1] "a"(qoff1), [kdma_lo] "s"(su((uint32_t)kdma)),            \
+  [qbase_lo] "s"(su((uint32_t)qbase)), [qbase_hi] "s"(su((uint32_t)(qbase >> 32))), [kdma_lo] "s"(su((uint32_t)kdma)), \
       [kdma_hi] "s"(su((uint32_t)(kdma >> 32))), [vdma_lo] "s"(su((uint32_t)vdma)),                               \
       [vdma_hi] "s"(su((uint32_t)(vdma >> 32))), [lds_k] "s"(su(lds_k)), [lds_v] "s"(su(lds_v)),                   \
       [nkt] "s"(su(nkt)), [valid_last] "s"(su(valid_last)), [ktile] "s"(su(ktile)), [wave1k] "s"(su(wave1k)),      \
@@ -125,7 +125,7 @@ __device__ __forceinline__ int padded_key_start(const int32_t* __restrict__ cu, 
       [koff0] "a"(koff[0]), [koff1] "a"(koff[1]), [koff2] "a"(koff[2]), [koff3] "a"(koff[3]),                     \
       [koffl0] "a"(koffl[0]), [koffl1] "a"(koffl[1]), [koffl2] "a"(koffl[2]), [koffl3] "a"(koffl[3]),             \
       [voff0] "v"(voff[0]), [voff1] "v"(voff[1]), [voff2] "v"(voff[2]), [voff3] "v"(voff[3]),                     \
-      [xaddr] "a"(xaddr), [hh8] "a"(hh8), [lane] "a"(lanev), [qrow0] "a"(qrow0), [qrow1] "a"(qrow1)
+      [lane] "a"(lanev), [qrow0] "a"(qrow0), [qrow1] "a"(qrow1)
 // Joint sources (with pre-scaled q): the two K and O source bases of the segment
 // (the text ones shifted back by len_img rows), len_img, the segment's first
 // joint row, per-lane Q row addresses and the K rows of each DMA instruction
@@ -190,10 +190,9 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
   const int nkt = (k_len + BN - 1) / BN;
   const int valid_last = k_len - (nkt - 1) * BN;
   const int pk = padded_key_start(cu_k, seg);
-  // Q rows past the segment end read its last row (their outputs are not stored)
+  // Q rows past the segment end read its last row (their outputs are not stored);
+  // the body forms each lane's 64-bit row address from qbase, its row and ldq
   const uint64_t qbase = (uint64_t)(uintptr_t)(Q + (int64_t)head * HD);
-  const uint32_t qoff0 = (uint32_t)((int64_t)min(qrow0, q_end - 1) * ldq * 2 + hh * 16);
-  const uint32_t qoff1 = (uint32_t)((int64_t)min(qrow1, q_end - 1) * ldq * 2 + hh * 16);
   uint64_t kdma = (uint64_t)(uintptr_t)(Kp + (int64_t)head * HD + (int64_t)k_beg * ldk);
   // joint: row j of the segment is row a0 + j of the "a" (image) operands while
   // j < len_a, else row b0 + j - len_a of the "b" (text) operands
@@ -248,8 +247,6 @@ __global__ __launch_bounds__(256, 1) void flash_fwd_asm(
     voff[i] = (uint32_t)((int64_t)(g * 8 + lrow) * vt_ld + ((g & 1) ? lsw1 : lsw0)) * 2;
   }
   const uint32_t wave1k = (uint32_t)wave_u * 1024u;
-  const uint32_t xaddr = (uint32_t)((lane ^ 32) * 4);
-  const uint32_t hh8 = (uint32_t)(hh * 8);
   const uint32_t lanev = (uint32_t)lane;
   const uint64_t obase = (uint64_t)(uintptr_t)(O + (int64_t)head * HD);
   const uint32_t ldob = (uint32_t)(ldo * 2);
@@ -416,7 +413,8 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
   DITK_REQUIRE(ldk < (1ll << 24) && vt_ld < (1ll << 24), "ditk_flash_attn_varlen: ldk / vt_ld too large");
   if (Tq == 0) return 0;
   const int64_t hs = (int64_t)head_dim * vt_ld;
-  DITK_REQUIRE((int64_t)Tq * ldq * 2 < (1ll << 32) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
+  // Q and O rows are addressed in 64 bits; the lse rows and tile offsets in 32
+  DITK_REQUIRE(Tq < (1 << 30) && ldk < (1ll << 23) && vt_ld < (1ll << 23),
                "ditk_flash_attn_varlen: tensor too large for 32-bit lane offsets");
   // passes per work item: several query tiles per workgroup when the segments
   // have few keys (vt_ld / nseg bounds the mean key count from above), so the

@@ -150,6 +150,36 @@ def sp(n):
     return f"s[{n}:{n + 1}]"
 
 
+def xaddr_to(g, dst, lane=None):
+    """VGPR dst = the ds_bpermute byte address of lane ^ 32 (the other half-wave);
+    lane: a VGPR already holding the lane index, else the operand."""
+    src = lane if lane is not None else opnd(g, "lane", dst)
+    g(f"v_xor_b32 {vr(dst)}, 32, {src}")
+    g(f"v_lshlrev_b32 {vr(dst)}, 2, {vr(dst)}")
+    return vr(dst)
+
+
+def hh8_to(g, dst):
+    """VGPR dst = 8 (lane / 32): this half-wave's key offset in a 16-key group."""
+    g(f"v_lshrrev_b32 {vr(dst)}, 5, {opnd(g, 'lane', dst)}")
+    g(f"v_lshlrev_b32 {vr(dst)}, 3, {vr(dst)}")
+    return vr(dst)
+
+
+def q_row_addr(g, row, a, t):
+    """VGPRs a, a + 1 (a even) = the 64-bit address of this lane's 16 bytes of Q row `row`
+    (VGPR, already clamped into the segment): qbase + row * ldq + 16 (lane / 32)
+    bytes.  t: a free VGPR.  64-bit, so the packed Q may exceed 4 GiB."""
+    g(f"v_mad_u64_u32 {vr(a, 2)}, {sp(S_CMP)}, {vr(row)}, %[ldqb], 0")
+    g(f"v_add_co_u32 {vr(a)}, vcc, %[qbase_lo], {vr(a)}")
+    g(f"v_mov_b32 {vr(t)}, %[qbase_hi]")
+    g(f"v_addc_co_u32 {vr(a + 1)}, vcc, {vr(t)}, {vr(a + 1)}, vcc")
+    g(f"v_lshrrev_b32 {vr(t)}, 5, {opnd(g, 'lane', t)}")
+    g(f"v_lshlrev_b32 {vr(t)}, 4, {vr(t)}")
+    g(f"v_add_co_u32 {vr(a)}, vcc, {vr(t)}, {vr(a)}")
+    g(f"v_addc_co_u32 {vr(a + 1)}, vcc, 0, {vr(a + 1)}, vcc")
+
+
 def vr(lo, n=1):
     return f"v{lo}" if n == 1 else f"v[{lo}:{lo + n - 1}]"
 
@@ -454,7 +484,7 @@ def row_max_to(g, s_set, qb, dst, tmp, atmp):
             g(f"v_max_f32 {vr(dst)}, {vr(dst)}, {vr(b)}")
         else:
             g(f"v_max3_f32 {vr(dst)}, {vr(dst)}, {vr(a)}, {vr(b)}")
-    xa = opnd(g, "xaddr", atmp)
+    xa = xaddr_to(g, atmp)
     g(f"ds_bpermute_b32 {vr(tmp)}, {xa}, {vr(dst)}")
     g("s_waitcnt lgkmcnt(0)")
     g(f"v_max_f32 {vr(dst)}, {vr(dst)}, {vr(tmp)}")
@@ -475,7 +505,7 @@ def softmax_tile(g, s_set, p_set, qb, kks, rs_dst, masked=False):
     """Recompute P for the given key halves of query block qb from the raw scores
     and the running m (pre: from S = q.k - m); rs_dst += sum (masked: keys >=
     valid excluded)."""
-    hh8 = opnd(g, "hh8", TMP + 3) if masked else None
+    hh8 = hh8_to(g, TMP + 3) if masked else None
     for kk in kks:
         for j in range(2):
             for e in range(4):
@@ -634,16 +664,14 @@ def last_tile_prefetch(g, a, nopf):
     tmp = S_SET[1 - a]  # S set of the next tile: free in the last tile
     g(f"s_add_u32 {s_(S_T0)}, {s_(S_QOFF)}, {BN * 4}")
     g(f"s_sub_u32 {s_(S_T1)}, %[qend], 1")
-    hh8 = opnd(g, "hh8", tmp + 2)
-    g(f"v_lshlrev_b32 {vr(tmp + 2)}, 1, {hh8}")
     for qb in range(2):
-        qrow = opnd(g, f"qrow{qb}", tmp + qb)
-        g(f"v_add_u32 {vr(tmp + qb)}, {s_(S_T0)}, {qrow}")
-        g(f"v_min_i32 {vr(tmp + qb)}, {s_(S_T1)}, {vr(tmp + qb)}")
-        g(f"v_mul_lo_u32 {vr(tmp + qb)}, {vr(tmp + qb)}, %[ldqb]")
-        g(f"v_add_u32 {vr(tmp + qb)}, {vr(tmp + qb)}, {vr(tmp + 2)}")
+        ad = tmp + 4 * qb  # even: the address pair, then the row and a temporary
+        qrow = opnd(g, f"qrow{qb}", ad + 2)
+        g(f"v_add_u32 {vr(ad + 2)}, {s_(S_T0)}, {qrow}")
+        g(f"v_min_i32 {vr(ad + 2)}, {s_(S_T1)}, {vr(ad + 2)}")
+        q_row_addr(g, ad + 2, ad, ad + 3)
         for c in range(NC):
-            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(tmp + qb)}, %[qbase] offset:{c * 32}")
+            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(ad, 2)}, off offset:{c * 32}")
     first_k_dmas(g)
     if a == 1:
         first_vt_dma(g)
@@ -800,9 +828,14 @@ def prologue(g, empty):
             for c in range(NC):
                 g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(qa, 2)}, off offset:{c * 32}")
             continue
-        qo = opnd(g, f"qoff{qb}", S_SET[0] + qb)
+        # this lane's row, the segment's last row for the rows past its end
+        ad = S_SET[0] + 4 * qb  # even: the address pair, then the row and a temporary
+        g(f"s_sub_u32 {s_(S_T1)}, %[qend], 1")
+        qrow = opnd(g, f"qrow{qb}", ad + 2)
+        g(f"v_min_i32 {vr(ad + 2)}, {s_(S_T1)}, {qrow}")
+        q_row_addr(g, ad + 2, ad, ad + 3)
         for c in range(NC):
-            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {qo}, %[qbase] offset:{c * 32}")
+            g(f"global_load_dwordx4 {ar(q_reg(qb, c), 4)}, {vr(ad, 2)}, off offset:{c * 32}")
     first_k_dmas(g)
     first_vt_dma(g)
     # O = 0, l = 0 while the loads fly
@@ -892,7 +925,7 @@ def epilogue(g, negm_of=None):
     g(f"s_lshl_b32 {s_(S_T1)}, %[ldob], {rpr.bit_length() - 1}")   # rpr rows of output
     for qb in range(2):
         lt, inv, t = EPI_L + 0, EPI_L + 1, EPI_L + 2
-        xa = opnd(g, "xaddr", EPI_L + 3)
+        xa = xaddr_to(g, EPI_L + 3, lane)
         qrow = vr(EB + 51)  # this lane's query row in this pass
         g(f"v_add_u32 {qrow}, {s_(S_QOFF)}, {opnd(g, f'qrow{qb}', EPI_L + 4)}")
         g(f"ds_bpermute_b32 {vr(t)}, {xa}, {vr(LRUN + qb)}")

@@ -7,12 +7,15 @@
   the CFG pair packed as 2 x 27280 tokens (text valid 150 / 0, t = 700) gives finite
   outputs, each segment bitwise equal to its solo forward.
 * Two blocks of the Wan2.1-T2V-14B architecture over the same 480p CFG pair,
-  packed bitwise equal to solo.
+  packed bitwise equal to solo; its 720p CFG pair's self-attention with q rows
+  past 4 GiB of offsets, on sampled rows against an fp32 reference.
 * One Wan2.2-5B block at 4096 tokens, one Wan2.1-14B block at 128 tokens and one
   Wan2.1 block at the full 21x30x52 grid (32760 tokens) against the CPU fp32
   oracle (torch's CPU flash SDPA for the 32760-token self-attention), cos >= 0.999
   and relative L2 <= 1e-2.
 """
+import math
+
 import pytest
 import torch
 
@@ -79,6 +82,44 @@ def test_wan21_14b_two_blocks_480p_cfg_pair_bitwise():
         assert out.shape == (16, 21, 60, 104) and bool(torch.isfinite(out).all())
         assert torch.equal(out, model.forward_packed([lat], [999.0], [txt])[0])
     assert not torch.equal(both[0], both[1])
+
+
+def test_attention_q_rows_past_4gib():
+    """Self-attention of a Wan2.1-14B CFG pair at 720x1280x81 (2 x 75600 tokens, 40
+    heads of 128) with q, k, v as column slices of one fused [151200, 3 x 5120] bf16
+    QKV buffer: q's rows span 4.6 GB, so rows near the end lie past 4 GiB of byte
+    offsets.  Sampled rows (heads 0 and 39; the first rows of segment 0, the last of
+    segment 1) against an fp32 reference, through the plain entry point and, after q
+    is scaled in place, the pre-scaled one."""
+    from ditserve_amd import ops
+    H, Dh, S = 40, 128, 75600
+    D, T = H * Dh, 2 * S
+    g = torch.Generator(device=DEV).manual_seed(5)
+    qkv = torch.empty((T, 3 * D), dtype=torch.bfloat16, device=DEV)
+    for i in range(0, T, 8192):
+        n = min(8192, T - i)
+        qkv[i:i + n] = torch.randn((n, 3 * D), generator=g, device=DEV).bfloat16()
+    q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    assert (T - 1) * q.stride(0) * 2 >= 2 ** 32
+    seg = ops.Segments([0, S, T], DEV)
+    rows = {0: torch.arange(0, 48, device=DEV), 1: torch.arange(T - 48, T, device=DEV)}
+    refs = {}
+    for m, r in rows.items():
+        for h in (0, H - 1):
+            cols = slice(h * Dh, (h + 1) * Dh)
+            kk, vv = k[m * S:(m + 1) * S, cols].float(), v[m * S:(m + 1) * S, cols].float()
+            p = torch.softmax(q[r, cols].float() @ kk.t() / math.sqrt(Dh), dim=-1)
+            refs[(m, h)] = p @ vv
+    out = ops.flash_attn_varlen(q, k, v, seg, seg, H, Dh)
+    for (m, h), ref in refs.items():
+        assert_close(out[rows[m], h * Dh:(h + 1) * Dh].float().cpu(), ref.cpu(), 0.9999, 1e-2, f"plain seg {m} head {h}")
+    del out
+    qkv[:, :D] = (q.float() * (ops.LOG2E / math.sqrt(Dh))).bfloat16()
+    vt = ops.transpose_v(v, H, Dh, seg)
+    out = ops.flash_attn_varlen(q, k, None, seg, seg, H, Dh, vt=vt, q_prescaled=True)
+    for (m, h), ref in refs.items():
+        # q rounded to bf16 once more after the scaling: a looser bound
+        assert_close(out[rows[m], h * Dh:(h + 1) * Dh].float().cpu(), ref.cpu(), 0.999, 2e-2, f"pre seg {m} head {h}")
 
 
 def _block_vs_oracle(cfg, grid, text_valid, t, seed, attn, label):

@@ -6,9 +6,10 @@
 * Wan2.2-TI2V-5B architecture, 30 blocks, latent 48x31x44x80 (704x1280x121 frames):
   the CFG pair packed as 2 x 27280 tokens (text valid 150 / 0, t = 700) gives finite
   outputs, each segment bitwise equal to its solo forward.
-* Two blocks of the Wan2.1-T2V-14B architecture over the same 480p CFG pair,
-  packed bitwise equal to solo; its 720p CFG pair's self-attention with q rows
-  past 4 GiB of offsets, on sampled rows against an fp32 reference.
+* Two blocks of the Wan2.1-T2V-14B architecture over its 720x1280x81 CFG pair (2 x
+  75600 tokens, a 4.6 GB fused QKV buffer), packed bitwise equal to solo; that
+  pair's self-attention with q rows past 4 GiB of offsets, on sampled rows against
+  an fp32 reference.
 * One Wan2.2-5B block at 4096 tokens, one Wan2.1-14B block at 128 tokens and one
   Wan2.1 block at the full 21x30x52 grid (32760 tokens) against the CPU fp32
   oracle (torch's CPU flash SDPA for the 32760-token self-attention), cos >= 0.999
@@ -66,20 +67,20 @@ def test_wan21_30_blocks_480p_cfg_pair_bitwise():
     assert not torch.equal(both[0], both[1])
 
 
-def test_wan21_14b_two_blocks_480p_cfg_pair_bitwise():
+def test_wan21_14b_two_blocks_720p_cfg_pair_bitwise():
     """Two blocks of the Wan2.1-T2V-14B architecture (hidden 5120, 40 heads, FFN
-    13824) over the 480p CFG pair packed as 2 x 32760 tokens: the fused QKV rows are
-    15360 wide and the GEMMs run K = 5120 and 13824 at M = 65520.  Each segment is
-    bitwise its solo forward."""
+    13824) over the 720x1280x81 CFG pair packed as 2 x 75600 tokens: the fused QKV
+    buffer (15360 wide) holds 4.6 GB, the GEMMs run K = 5120 and 13824 at
+    M = 151200.  Each segment is bitwise its solo forward."""
     import dataclasses
 
     from ditserve_amd.wan import WAN21_T2V_14B, WanTransformer
     model = WanTransformer.random(dataclasses.replace(WAN21_T2V_14B, layers=2), seed=11, device=DEV)
-    lat = randn((16, 21, 60, 104), 54).to(DEV)
+    lat = randn((16, 21, 90, 160), 54).to(DEV)
     tc, tu = _text(55, 120).to(DEV), torch.zeros(512, 4096, device=DEV)
     both = model.forward_packed([lat, lat], [999.0, 999.0], [tc, tu])
     for out, txt in zip(both, (tc, tu)):
-        assert out.shape == (16, 21, 60, 104) and bool(torch.isfinite(out).all())
+        assert out.shape == (16, 21, 90, 160) and bool(torch.isfinite(out).all())
         assert torch.equal(out, model.forward_packed([lat], [999.0], [txt])[0])
     assert not torch.equal(both[0], both[1])
 

@@ -24,7 +24,9 @@ attention roofline fraction and CPU baseline:
                           4 x 512^2 requests, each a CFG pair (12 joint segments),
                           per-request FlowMatch-Euler;
   * wan22_ti2v_5b_704p_cfg2  Wan2.2-TI2V-5B 704x1280x121f step, CFG pair of
-                          2 x 27280 tokens, text valid 150/0, t = 700 schedule.
+                          2 x 27280 tokens, text valid 150/0, t = 700 schedule;
+  * wan21_720p_cfg2       Wan2.1-T2V-1.3B 720x1280x81f step, CFG pair of 2 x 75600
+                          tokens (latent 16x21x90x160), UniPC flow shift 5.
 
 Prints one JSON line.  ``roofline`` is for the dominant kernel, the self-attention
 flash kernel, from HIP events recorded on its launch stream over the timed steps.
@@ -57,6 +59,9 @@ WORKLOADS = {
     "wan21_480p": dict(
         metric=WAN21_METRIC, arch="wan21", latent=(16, 21, 60, 104), text_valid=(120, 0), flow_shift=3.0,
         ref_ms=3964.62),
+    "wan21_720p": dict(
+        metric="denoise steps/s & tokens/s, Wan2.1-1.3B 720p-81f CFG2; attn % bf16 MFMA peak",
+        arch="wan21", latent=(16, 21, 90, 160), text_valid=(120, 0), flow_shift=5.0, ref_ms=16212.46),
     "wan22_ti2v_5b_704p": dict(
         metric="denoise steps/s & tokens/s, Wan2.2-TI2V-5B 704p-121f CFG2; attn % bf16 MFMA peak",
         arch="wan22", latent=(48, 31, 44, 80), text_valid=(150, 0), flow_shift=5.0, ref_ms=7813.18),
@@ -410,7 +415,8 @@ def run_wan_cfg(name, steps, warmup, breakdown=False):
     attn_flops = 4.0 * 2 * seq * seq * cfg.dim  # per launch: 2 segments (CFG pair), non-causal
     total_flops = step_flops(cfg, [seq, seq], cfg.text_len)
     arch = "Wan2.1-T2V-1.3B" if wl["arch"] == "wan21" else "Wan2.2-TI2V-5B"
-    frames = "480x832x81f" if wl["arch"] == "wan21" else "704x1280x121f"
+    vae = 8 if wl["arch"] == "wan21" else 16  # the VAE's spatial stride; 4 frames per latent frame
+    frames = f"{latent_shape[2] * vae}x{latent_shape[3] * vae}x{(latent_shape[1] - 1) * 4 + 1}f"
     out = {
         "metric": wl["metric"], "value": 1000.0 / ms, "unit": "steps/s", "steps": steps, "warmup": warmup,
         "ms_per_step": ms, "tokens_per_s": 2 * seq * 1000.0 / ms,
@@ -789,7 +795,7 @@ def main():
     if not args.no_per_config:
         per = {}
         plan = [("wan21_480p", 3, 1), ("wan21_packed_4req", 5, 2), ("sd35_medium_1024", 10, 3),
-                ("sd35_packed_2x1024_4x512", 5, 2), ("wan22_ti2v_5b_704p", 3, 1)]
+                ("sd35_packed_2x1024_4x512", 5, 2), ("wan22_ti2v_5b_704p", 3, 1), ("wan21_720p", 2, 1)]
         for name, steps, warmup in plan:
             if name == args.workload:
                 res = dict(head)
@@ -803,7 +809,7 @@ def main():
             key = {"wan21_480p": "wan21_480p_cfg2", "wan21_packed_4req": "wan21_packed_4req",
                    "sd35_medium_1024": "sd35_medium_1024_cfg2",
                    "sd35_packed_2x1024_4x512": "sd35_packed_2x1024_4x512_cfg2",
-                   "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2"}[name]
+                   "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2", "wan21_720p": "wan21_720p_cfg2"}[name]
             res.pop("breakdown_ms_per_step", None)
             per[key] = _public(res)
             print(f"[bench] {key}: {res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)

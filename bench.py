@@ -26,7 +26,9 @@ attention roofline fraction and CPU baseline:
   * wan22_ti2v_5b_704p_cfg2  Wan2.2-TI2V-5B 704x1280x121f step, CFG pair of
                           2 x 27280 tokens, text valid 150/0, t = 700 schedule;
   * wan21_720p_cfg2       Wan2.1-T2V-1.3B 720x1280x81f step, CFG pair of 2 x 75600
-                          tokens (latent 16x21x90x160), UniPC flow shift 5.
+                          tokens (latent 16x21x90x160), UniPC flow shift 5;
+  * wan21_480p_33f_cfg2   Wan2.1-T2V-1.3B 480x832x33f step (the reference's dev
+                          shape), CFG pair of 2 x 14040 tokens.
 
 Prints one JSON line.  ``roofline`` is for the dominant kernel, the self-attention
 flash kernel, from HIP events recorded on its launch stream over the timed steps.
@@ -59,6 +61,9 @@ WORKLOADS = {
     "wan21_480p": dict(
         metric=WAN21_METRIC, arch="wan21", latent=(16, 21, 60, 104), text_valid=(120, 0), flow_shift=3.0,
         ref_ms=3964.62),
+    "wan21_480p_33f": dict(
+        metric="denoise steps/s & tokens/s, Wan2.1-1.3B 480p-33f CFG2; attn % bf16 MFMA peak",
+        arch="wan21", latent=(16, 9, 60, 104), text_valid=(120, 0), flow_shift=3.0, ref_ms=1149.62),
     "wan21_720p": dict(
         metric="denoise steps/s & tokens/s, Wan2.1-1.3B 720p-81f CFG2; attn % bf16 MFMA peak",
         arch="wan21", latent=(16, 21, 90, 160), text_valid=(120, 0), flow_shift=5.0, ref_ms=16212.46),
@@ -795,7 +800,8 @@ def main():
     if not args.no_per_config:
         per = {}
         plan = [("wan21_480p", 3, 1), ("wan21_packed_4req", 5, 2), ("sd35_medium_1024", 10, 3),
-                ("sd35_packed_2x1024_4x512", 5, 2), ("wan22_ti2v_5b_704p", 3, 1), ("wan21_720p", 2, 1)]
+                ("sd35_packed_2x1024_4x512", 5, 2), ("wan22_ti2v_5b_704p", 3, 1), ("wan21_720p", 2, 1),
+                ("wan21_480p_33f", 5, 2)]
         for name, steps, warmup in plan:
             if name == args.workload:
                 res = dict(head)
@@ -809,7 +815,8 @@ def main():
             key = {"wan21_480p": "wan21_480p_cfg2", "wan21_packed_4req": "wan21_packed_4req",
                    "sd35_medium_1024": "sd35_medium_1024_cfg2",
                    "sd35_packed_2x1024_4x512": "sd35_packed_2x1024_4x512_cfg2",
-                   "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2", "wan21_720p": "wan21_720p_cfg2"}[name]
+                   "wan22_ti2v_5b_704p": "wan22_ti2v_5b_704p_cfg2", "wan21_720p": "wan21_720p_cfg2",
+                   "wan21_480p_33f": "wan21_480p_33f_cfg2"}[name]
             res.pop("breakdown_ms_per_step", None)
             per[key] = _public(res)
             print(f"[bench] {key}: {res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)

@@ -50,6 +50,15 @@ def to_device(data, dtype, device):
     return host.pin_memory().to(device, non_blocking=True)
 
 
+def _vec(t, name, n):
+    """An fp32 per-feature vector (norm weight, bias): 1-D, n long, unit stride (the
+    kernels read it as a contiguous array)."""
+    _check(t, name, torch.float32, 1)
+    if t.shape[0] != n or (n > 1 and t.stride(0) != 1):
+        raise ValueError(f"{name} must be a contiguous [{n}] vector, got shape {tuple(t.shape)} "
+                         f"stride {t.stride()}")
+
+
 def _rows(t, name):
     """2-D row-major view requirements: unit column stride, 16-byte aligned rows."""
     if t.dim() != 2 or t.stride(1) != 1:
@@ -235,6 +244,8 @@ def _adaln_job(x, shift=None, scale=None, segments=None, weight=None, bias=None,
     mod_stride = 0
     cu = None
     nseg = 0
+    if (shift is None) != (scale is None):
+        raise ValueError("shift and scale go together")
     if shift is not None:
         _check(shift, "shift", torch.float32, 2)
         _check(scale, "scale", torch.float32, 2)
@@ -250,9 +261,7 @@ def _adaln_job(x, shift=None, scale=None, segments=None, weight=None, bias=None,
         cu, nseg = segments.dev, segments.nseg
     for t, n in ((weight, "weight"), (bias, "bias")):
         if t is not None:
-            _check(t, n, torch.float32, 1)
-            if t.shape[0] != D:
-                raise ValueError(f"{n} must be [{D}]")
+            _vec(t, n, D)
     if kind not in ("ln", "rms"):
         raise ValueError(f"kind must be 'ln' or 'rms', got {kind!r}")
     job = _lib.AdalnJob(_ptr(x), ldx, _ptr(out), ldy, _ptr(cu), _ptr(shift), _ptr(scale), mod_stride, _ptr(weight),
@@ -324,9 +333,7 @@ def qk_norm_multi(jobs):
             raise ValueError("q and k must have the same shape")
         T, D = q.shape
         for t, n in ((wq, "wq"), (wk, "wk")):
-            _check(t, n, torch.float32, 1)
-            if t.shape[0] != D:
-                raise ValueError(f"{n} must be [{D}]")
+            _vec(t, n, D)
         qo, ko = j.get("out") or (q, k)
         for t, n in ((qo, "q_out"), (ko, "k_out")):
             _check(t, n, _BF16, 2)
@@ -357,9 +364,7 @@ def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None, o
     T, D = q.shape
     ldq, ldk = _rows(q, "q"), _rows(k, "k")
     for t, n in ((wq, "wq"), (wk, "wk")):
-        _check(t, n, torch.float32, 1)
-        if t.shape[0] != D:
-            raise ValueError(f"{n} must be [{D}]")
+        _vec(t, n, D)
     if rope is None:
         args = (None, None, 0, None, None, 0, 0, 0)
     else:
@@ -397,9 +402,7 @@ def _linear_args(x, w, b, epilogue, residual, gate, segments, out):
         raise ValueError(f"weight is {tuple(w.shape)}, input has K={K}")
     lda, ldw = _rows(x, "x"), _rows(w, "w")
     if b is not None:
-        _check(b, "bias", torch.float32, 1)
-        if b.shape[0] != N:
-            raise ValueError("bias size mismatch")
+        _vec(b, "bias", N)
     if epilogue not in EPILOGUES:
         raise ValueError(f"unknown epilogue {epilogue!r}")
     odt = torch.float32 if epilogue == "f32" else _BF16

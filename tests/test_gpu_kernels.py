@@ -811,4 +811,11 @@ def test_invalid_arguments_raise_before_launch():
         ops.cfg_combine(torch.zeros(8, device=DEV), torch.zeros(6, device=DEV), 5.0)
     with pytest.raises(DitkError):  # rows wider than the row kernels hold in registers (6144)
         ops.adaln(torch.zeros((4, 6152), dtype=torch.bfloat16, device=DEV))
+    xr = torch.zeros((4, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):  # a strided weight view (the kernel reads a contiguous vector)
+        ops.adaln(xr, weight=torch.ones(128, device=DEV)[::2])
+    with pytest.raises(ValueError):  # scale without shift
+        ops.adaln(xr, scale=torch.zeros((1, 64), device=DEV), segments=_seg([0, 4]))
+    with pytest.raises(ValueError):  # a strided bias
+        ops.linear(xr, torch.zeros((64, 64), dtype=torch.bfloat16, device=DEV), torch.zeros(128, device=DEV)[::2])
     torch.cuda.synchronize()

@@ -290,6 +290,13 @@ class Rope:
     [max_pos, head_dim/2] fp32 (float64-built), per-segment (F', H', W') grids."""
 
     def __init__(self, cos_tab, sin_tab, grids, segments, t_pairs, h_pairs):
+        for t, n in ((cos_tab, "cos table"), (sin_tab, "sin table")):
+            _check(t, n, torch.float32, 2)
+            if not t.is_contiguous() or t.shape != cos_tab.shape:
+                raise ValueError("the cos and sin tables must be contiguous [max_pos, head_dim / 2] fp32")
+        for g in grids:
+            if max(g) > cos_tab.shape[0]:
+                raise ValueError(f"grid {tuple(g)} reaches past the {cos_tab.shape[0]}-position RoPE tables")
         self.cos, self.sin = cos_tab, sin_tab
         self.grids = to_device([list(map(int, g)) for g in grids], torch.int32, cos_tab.device).reshape(-1)
         self.segments = segments
@@ -370,6 +377,8 @@ def qk_norm_rope_(q, k, wq, wk, head_dim, eps=1e-6, per_head=False, rope=None, o
     else:
         if rope.segments.total != T:
             raise ValueError("rope segments do not cover q")
+        if rope.cos.shape[1] != head_dim // 2:
+            raise ValueError(f"RoPE tables hold {rope.cos.shape[1]} pairs, head_dim {head_dim} needs {head_dim // 2}")
         args = (_ptr(rope.cos), _ptr(rope.sin), rope.cos.shape[0], _ptr(rope.segments.dev), _ptr(rope.grids),
                 rope.segments.nseg, rope.t_pairs, rope.h_pairs)
     if out is None:

@@ -816,6 +816,14 @@ def test_invalid_arguments_raise_before_launch():
         ops.adaln(xr, weight=torch.ones(128, device=DEV)[::2])
     with pytest.raises(ValueError):  # scale without shift
         ops.adaln(xr, scale=torch.zeros((1, 64), device=DEV), segments=_seg([0, 4]))
+    from ditserve_amd.wan import rope_tables
+    cos_t, sin_t = rope_tables(128, 16, 10000.0, DEV)
+    with pytest.raises(ValueError):  # a grid longer than the 16-position RoPE tables
+        ops.Rope(cos_t, sin_t, [(2, 20, 1)], _seg([0, 40]), 22, 21)
+    with pytest.raises(ValueError):  # tables for head_dim 128 on head_dim-64 rows
+        q64 = torch.zeros((40, 128), dtype=torch.bfloat16, device=DEV)
+        ops.qk_norm_rope_(q64, q64.clone(), torch.ones(128, device=DEV), torch.ones(128, device=DEV), 64,
+                          rope=ops.Rope(cos_t, sin_t, [(2, 4, 5)], _seg([0, 40]), 22, 21))
     with pytest.raises(ValueError):  # a strided bias
         ops.linear(xr, torch.zeros((64, 64), dtype=torch.bfloat16, device=DEV), torch.zeros(128, device=DEV)[::2])
     torch.cuda.synchronize()

@@ -356,8 +356,14 @@ class SD35Transformer:
         for l in lats:
             if l.shape[0] != cfg.in_ch or l.shape[1] % P or l.shape[2] % P:
                 raise ValueError(f"latent {tuple(l.shape)} must be [{cfg.in_ch}, H, W] with H, W divisible by {P}")
+            if max(l.shape[1], l.shape[2]) // P > cfg.pos_max:
+                raise ValueError(f"latent {tuple(l.shape)} has more than pos_embed_max_size = {cfg.pos_max} patches "
+                                 "along a side")
             hw.append((l.shape[1] // P, l.shape[2] // P))
         img_counts = [a * b for a, b in hw]
+        for t in texts:
+            if t.dim() < 2 or t.shape[-1] != cfg.text_dim:
+                raise ValueError(f"text contexts must be [L, {cfg.text_dim}], got {tuple(t.shape)}")
         txts = [t.reshape(-1, cfg.text_dim) for t in texts]
         txt_counts = [t.shape[0] for t in txts]
         lay = joint_layout(img_counts, txt_counts)

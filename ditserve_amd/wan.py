@@ -249,13 +249,19 @@ class WanTransformer:
         cfg, dev = self.cfg, self.device
         if not (len(latents) == len(timesteps) == len(texts)) or not latents:
             raise ValueError("latents, timesteps and texts must be non-empty lists of equal length")
+        for t in texts:
+            if t.dim() < 2 or t.shape[-1] != cfg.text_dim:
+                raise ValueError(f"text contexts must be [L, {cfg.text_dim}], got {tuple(t.shape)}")
+        for lat in latents:
+            if lat.dim() < 4 or lat.shape[-4] != cfg.in_ch:
+                raise ValueError(f"latents must be [{cfg.in_ch}, F, H, W], got {tuple(lat.shape)}")
         grids = [self._grid(l.shape) for l in latents]
         counts = [g[0] * g[1] * g[2] for g in grids]
         seg = Segments([0] + [sum(counts[: i + 1]) for i in range(len(counts))], dev)
         hidden = torch.empty((seg.total, cfg.dim), dtype=_BF16, device=dev)
         cache = {}
         for i, lat in enumerate(latents):
-            key = (lat.data_ptr(), tuple(lat.shape))
+            key = (lat.data_ptr(), tuple(lat.shape), tuple(lat.stride()), lat.dtype, lat.device)
             if key in cache:  # CFG pairs share the latent: patchify once
                 hidden[seg.cu[i]:seg.cu[i + 1]] = hidden[cache[key][0]:cache[key][1]]
                 continue

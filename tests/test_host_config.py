@@ -88,3 +88,25 @@ def test_view_extent_and_overlap():
     assert ops._extent(cols) == (cols.data_ptr(), cols.data_ptr() + (9 * 8 + 2) * 2)
     assert ops._overlap(cols, base[9:]) and not ops._overlap(base[:, :2][:1], base[:, 2:4][:1])
     assert ops._extent(base[:0]) == (0, 0) and not ops._overlap(base[:0], base)
+
+
+def test_model_inputs_refused_before_any_launch():
+    """Wrong latent channels / grids, text widths or SD3 patch counts raise
+    ValueError before the first kernel (checked here on the CPU, no library call)."""
+    import torch
+
+    from ditserve_amd import sd35, wan
+    w = wan.WanTransformer.__new__(wan.WanTransformer)
+    w.cfg, w.device = wan.WAN21_T2V_1_3B, "cpu"
+    lat = torch.zeros(16, 3, 8, 8)
+    for lats, texts in (([torch.zeros(4, 3, 8, 8)], [torch.zeros(512, 4096)]),   # channels
+                        ([torch.zeros(16, 3, 7, 8)], [torch.zeros(512, 4096)]),   # H not a patch multiple
+                        ([lat], [torch.zeros(512, 2048)]),                        # text width
+                        ([lat, lat], [torch.zeros(512, 4096)])):                  # list lengths
+        with pytest.raises(ValueError):
+            w.begin_packed_packet(lats, [500.0] * len(lats), texts)
+    s = sd35.SD35Transformer.__new__(sd35.SD35Transformer)
+    s.cfg, s.device = sd35.SD35_MEDIUM, "cpu"
+    for lat, txt in (((16, 800, 64), (10, 4096)), ((16, 64, 64), (10, 2048)), ((4, 64, 64), (10, 4096))):
+        with pytest.raises(ValueError):
+            s.forward_packed([torch.zeros(lat)], [1.0], [torch.zeros(txt)], [torch.zeros(2048)])

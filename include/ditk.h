@@ -179,7 +179,9 @@ int ditk_transpose_v(const void* v, int64_t ldv, void* vt, int64_t vt_ld, int Tk
  * Varlen block-diagonal flash attention forward (non-causal, no dropout):
  * segment m's queries [cu_q[m], cu_q[m+1]) attend to keys [cu_k[m], cu_k[m+1]).
  * head_dim 64 or 128; out bf16 [Tq, heads*head_dim]; lse (optional, may be NULL)
- * fp32 [heads][lse_ld], natural log of the softmax denominator.
+ * fp32 [heads][lse_ld], natural log of the softmax denominator.  Q and out rows
+ * are addressed in 64 bits (a packed Q may span more than 4 GiB); Tq < 2^30,
+ * ldk and vt_ld < 2^23.
  * Replaces: the attention backend call Spec.run -> sdpa/aiter kernels —
  *   workers/xfuser/core/attention/spec.py:283-304, backends/sdpa/kernel.py:30-56,
  *   backends/aiter/kernel.py:105-128 (via usp.py:815-824 and usp.py:875-908), and the

@@ -511,10 +511,12 @@ DITK_EXPORT int ditk_modulation(const float* table, const float* proj, float* mo
 
 namespace {
 int qk_norm_check(const void* q, int64_t ldq, const void* k, int64_t ldk, void* qo, int64_t ldqo, void* ko,
-                  int64_t ldko, int D, int head_dim, const float* wq, const float* wk, const float* rope_cos,
+                  int64_t ldko, int T, int D, int head_dim, const float* wq, const float* wk, const float* rope_cos,
                   const float* rope_sin, int max_pos, const int32_t* cu_seqlens, const int32_t* grids, int nseg,
                   int t_pairs, int h_pairs) {
-  DITK_REQUIRE(q && k && qo && ko && wq && wk, "ditk_qk_norm_rope: null tensor");
+  DITK_REQUIRE(T >= 0, "ditk_qk_norm_rope: bad T");
+  // the row tensors may be NULL when there are no rows
+  DITK_REQUIRE((T == 0 || (q && k && qo && ko)) && wq && wk, "ditk_qk_norm_rope: null tensor");
   DITK_REQUIRE(D > 0 && D % 8 == 0 && D <= 64 * 8 * kMaxChunks, "ditk_qk_norm_rope: bad D=%d", D);
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_qk_norm_rope: head_dim must be 64 or 128");
   DITK_REQUIRE(D % head_dim == 0, "ditk_qk_norm_rope: D %% head_dim != 0");
@@ -539,10 +541,9 @@ int qk_norm_rope_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, 
                         int per_head, const float* rope_cos, const float* rope_sin, int max_pos,
                         const int32_t* cu_seqlens, const int32_t* grids, int nseg, int t_pairs, int h_pairs,
                         hipStream_t stream) {
-  const int rc = qk_norm_check(q, ldq, k, ldk, qo, ldqo, ko, ldko, D, head_dim, wq, wk, rope_cos, rope_sin, max_pos,
-                               cu_seqlens, grids, nseg, t_pairs, h_pairs);
+  const int rc = qk_norm_check(q, ldq, k, ldk, qo, ldqo, ko, ldko, T, D, head_dim, wq, wk, rope_cos, rope_sin,
+                               max_pos, cu_seqlens, grids, nseg, t_pairs, h_pairs);
   if (rc) return rc;
-  DITK_REQUIRE(T >= 0, "ditk_qk_norm_rope: bad T");
   if (T == 0) return 0;
   dim3 grid((T + kRowsPerBlock - 1) / kRowsPerBlock);
   const int nc = (D / 8 + 63) / 64;
@@ -586,10 +587,9 @@ DITK_EXPORT int ditk_qk_norm_multi(const ditk_qk_norm_job* jobs, int njobs, hipS
   int64_t blocks = 0;
   for (int j = 0; j < njobs; ++j) {
     const ditk_qk_norm_job& p = jobs[j];
-    const int rc = qk_norm_check(p.q, p.ldq, p.k, p.ldk, p.q_out, p.ldqo, p.k_out, p.ldko, p.D, p.head_dim, p.wq,
+    const int rc = qk_norm_check(p.q, p.ldq, p.k, p.ldk, p.q_out, p.ldqo, p.k_out, p.ldko, p.T, p.D, p.head_dim, p.wq,
                                  p.wk, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0);
     if (rc) return rc;
-    DITK_REQUIRE(p.T >= 0, "ditk_qk_norm_multi: bad T");
     const int ncj = (p.D / 8 + 63) / 64;
     const int gj = !p.per_head ? 64 : (p.head_dim == 128 ? 16 : 8);
     DITK_REQUIRE(j == 0 || (ncj == nc && gj == group),

@@ -80,7 +80,9 @@ int ditk_modulation(const float* table, const float* proj, float* mod, int nseg,
  * by 3D RoPE on interleaved pairs (optional: rope_cos == NULL skips it).
  * rope tables: fp32 [max_pos][head_dim/2]; pair p rotates with the token's frame
  * position when p < t_pairs, row position when p < t_pairs + h_pairs, else column
- * position; grids: int32 [nseg][3] = (F', H', W') per segment.
+ * position; grids: int32 [nseg][3] = (F', H', W') per segment.  q and k may be
+ * NULL when T == 0 (nothing is launched); positions past max_pos read the last
+ * table row.
  * Replaces: _qk_norm_rope_reference and the fused_qk_norm_rope slot —
  *   transformer_wan.py:24-25,111-115,158-191; SD3.5 per-head norm_q/norm_k —
  *   sd35_batch.py:428-431,438-441.

@@ -410,6 +410,16 @@ def test_qk_norm_multi_matches_single_calls(per_head, Dh):
              out=(buf[:, :D], buf[:, 2 * D:]))])
     assert torch.equal(qkv_i, ref_i) and torch.equal(qkv_t, ref_t)
     assert torch.equal(got[2][0], ref_t[:, :D]) and torch.equal(got[2][1], ref_t[:, D:2 * D])
+    # zero-row jobs (empty views: NULL pointers) are skipped, alone or beside others
+    e = torch.empty((0, 3 * D), dtype=torch.bfloat16, device=DEV)
+    ops.qk_norm_rope_(e[:, :D], e[:, D:2 * D], *wt, Dh, per_head=per_head)
+    before = qkv_t.clone()
+    ops.qk_norm_multi([dict(q=e[:, :D], k=e[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh, per_head=per_head),
+                       dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=Dh,
+                            per_head=per_head)])
+    again = before.clone()
+    ops.qk_norm_rope_(again[:, :D], again[:, D:2 * D], *wt, Dh, per_head=per_head)
+    assert torch.equal(qkv_t, again)
     assert torch.equal(buf[:, D:2 * D], torch.zeros_like(buf[:, D:2 * D])) and torch.equal(src[:, 2 * D:],
                                                                                             qkv_t[:, 2 * D:])
     other = dict(q=qkv_t[:, :D], k=qkv_t[:, D:2 * D], wq=wt[0], wk=wt[1], head_dim=64 if Dh == 128 else 128,

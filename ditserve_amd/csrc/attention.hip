@@ -356,7 +356,7 @@ namespace {
 int transpose_launch(const void* v, const void* vb, int64_t ldv, void* vt, int64_t vt_ld, int Tk, int heads,
                      int head_dim, const int32_t* cu_k, const int32_t* cu_a, const int32_t* cu_b, int nseg,
                      hipStream_t stream) {
-  DITK_REQUIRE(v && vt && cu_k, "ditk_transpose_v: null tensor");
+  DITK_REQUIRE(cu_k && (Tk == 0 || (v && vt)), "ditk_transpose_v: null tensor");
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_transpose_v: head_dim must be 64 or 128");
   DITK_REQUIRE(nseg > 0 && heads > 0 && Tk >= 0, "ditk_transpose_v: bad sizes");
   DITK_REQUIRE(ldv % 8 == 0 && vt_ld % 8 == 0, "ditk_transpose_v: leading dims must be multiples of 8");
@@ -402,7 +402,8 @@ int flash_launch(const void* q, int64_t ldq, const void* k, int64_t ldk, const v
   DITK_REQUIRE(!joint || (pre && qb && kb && ob && cu_b), "ditk_joint_attn: needs both sources and both tables");
   DITK_REQUIRE(!joint || (((uintptr_t)qb % 16) == 0 && ((uintptr_t)kb % 16) == 0 && ((uintptr_t)ob % 8) == 0),
                "ditk_joint_attn: misaligned tensor");
-  DITK_REQUIRE(q && k && vt && o && cu_q && cu_k, "ditk_flash_attn_varlen: null tensor");
+  // q and o may be NULL when there are no queries (empty tensors)
+  DITK_REQUIRE(k && vt && cu_q && cu_k && (Tq == 0 || (q && o)), "ditk_flash_attn_varlen: null tensor");
   DITK_REQUIRE(head_dim == 64 || head_dim == 128, "ditk_flash_attn_varlen: head_dim must be 64 or 128, got %d", head_dim);
   DITK_REQUIRE(nseg > 0 && heads > 0 && Tq >= 0, "ditk_flash_attn_varlen: bad sizes");
   DITK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldo % 4 == 0 && vt_ld % 8 == 0,

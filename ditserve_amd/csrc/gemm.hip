@@ -813,7 +813,8 @@ namespace {
 int gemm_validate(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
                   int M, int N, int K, int epilogue, const void* R, int64_t ldr, const float* gate,
                   int64_t gate_stride, const int32_t* cu_seqlens, int nseg) {
-  DITK_REQUIRE(A && W && C, "ditk_gemm: null operand");
+  // A, C and R may be NULL when there are no rows (an empty tensor's pointer)
+  DITK_REQUIRE(W && (M == 0 || (A && C)), "ditk_gemm: null operand");
   DITK_REQUIRE(M >= 0 && N > 0 && K > 0, "ditk_gemm: bad shape M=%d N=%d K=%d", M, N, K);
   DITK_REQUIRE(K % 32 == 0, "ditk_gemm: K=%d must be a multiple of 32", K);
   DITK_REQUIRE(N % 8 == 0, "ditk_gemm: N=%d must be a multiple of 8", N);
@@ -827,7 +828,7 @@ int gemm_validate(const void* A, int64_t lda, const void* W, int64_t ldw, const 
   DITK_REQUIRE(ldc % 8 == 0 && ldc >= N, "ditk_gemm: ldc must be a multiple of 8 and >= N");
   DITK_REQUIRE(epilogue >= 0 && epilogue <= 5, "ditk_gemm: unknown epilogue %d", epilogue);
   DITK_REQUIRE(!(epilogue == EPI_GATE_RES || epilogue == EPI_RES) ||
-               (R && ldr % 8 == 0 && ldr >= N && ((uintptr_t)R % 16) == 0),
+               ((R || M == 0) && ldr % 8 == 0 && ldr >= N && ((uintptr_t)R % 16) == 0),
                "ditk_gemm: residual epilogue needs a 16-byte aligned R with ldr %% 8 == 0");
   DITK_REQUIRE(epilogue != EPI_GATE_RES || (gate_stride % 4 == 0 && ((uintptr_t)gate % 16) == 0),
                "ditk_gemm: gate rows must be 16-byte aligned");

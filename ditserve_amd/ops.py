@@ -572,15 +572,17 @@ def flash_attn_varlen(q, k, v, seg_q, seg_k, heads, head_dim, softmax_scale=None
         raise ValueError(f"out must be [{Tq}, {width}], got {tuple(out.shape)}")
     ldo = _rows(out, "out")
     lse = torch.empty((heads, Tq), dtype=torch.float32, device=q.device) if return_lse else None
+    # with no keys at all no K tile is read: any valid address stands in for the empty K
+    kp = _ptr(k) if k.shape[0] else _ptr(vt)
     if q_prescaled:
         if softmax_scale is not None:
             raise ValueError("q_prescaled carries the softmax scale in q: pass softmax_scale=None")
-        _lib.call("ditk_flash_attn_varlen_q_prescaled", _ptr(q), ldq, _ptr(k), ldk, _ptr(vt), vt.shape[2],
+        _lib.call("ditk_flash_attn_varlen_q_prescaled", _ptr(q), ldq, kp, ldk, _ptr(vt), vt.shape[2],
                   _ptr(out), ldo, _ptr(lse), Tq, _ptr(seg_q.dev), _ptr(seg_k.dev), seg_q.nseg, Tq, heads,
                   head_dim, _stream())
         return (out, lse) if return_lse else out
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
-    _lib.call("ditk_flash_attn_varlen", _ptr(q), ldq, _ptr(k), ldk, _ptr(vt), vt.shape[2], _ptr(out), ldo,
+    _lib.call("ditk_flash_attn_varlen", _ptr(q), ldq, kp, ldk, _ptr(vt), vt.shape[2], _ptr(out), ldo,
               _ptr(lse), Tq, _ptr(seg_q.dev), _ptr(seg_k.dev), seg_q.nseg, Tq, heads, head_dim, scale, _stream())
     return (out, lse) if return_lse else out
 

@@ -607,6 +607,24 @@ def test_attention_query_tile_passes_bitwise(Dh, pre, cu_k):
     assert bool(torch.all(lse[:, 32768:] == -math.inf))
 
 
+def test_empty_inputs_are_no_ops():
+    """Zero-row GEMM inputs and zero-query or zero-key attention calls (empty
+    tensors: NULL pointers) launch nothing and return empty or zero-filled outputs."""
+    ops = _ops()
+    w, b = torch.zeros((64, 64), dtype=torch.bfloat16, device=DEV), torch.zeros(64, device=DEV)
+    x0 = torch.empty((0, 64), dtype=torch.bfloat16, device=DEV)
+    assert ops.linear(x0, w, b).shape == (0, 64)
+    assert ops.linear(x0, w, b, "res", residual=torch.empty((0, 64), dtype=torch.bfloat16, device=DEV)).shape == (0, 64)
+    q0 = torch.empty((0, 128), dtype=torch.bfloat16, device=DEV)
+    kv = randn((40, 128), 3).to(DEV, torch.bfloat16)
+    assert ops.flash_attn_varlen(q0, kv, kv, _seg([0, 0]), _seg([0, 40]), 1, 128).shape == (0, 128)
+    q = randn((40, 128), 4).to(DEV, torch.bfloat16)
+    k0 = torch.empty((0, 128), dtype=torch.bfloat16, device=DEV)
+    out, lse = ops.flash_attn_varlen(q, k0, k0, _seg([0, 40]), _seg([0, 0]), 1, 128, return_lse=True)
+    assert torch.equal(out, torch.zeros_like(out)) and bool(torch.isneginf(lse).all())
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("Dh", [128, 64])
 @pytest.mark.parametrize("pre", [False, True])
 def test_attention_segments_without_keys(Dh, pre):

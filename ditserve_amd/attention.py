@@ -39,6 +39,16 @@ class VarlenPacking:
     cu_seqlens_k: torch.Tensor
     max_seqlen_k: int
 
+    @classmethod
+    def from_kwargs(cls, attention_kwargs):
+        """The packing a model put in its attention kwargs (keys ``indices_k``,
+        ``cu_seqlens_k``, ``max_seqlen_k``; spec.py:74-85), or None without
+        ``indices_k``."""
+        kw = attention_kwargs or {}
+        if kw.get("indices_k") is None:
+            return None
+        return cls(kw["indices_k"], kw["cu_seqlens_k"], kw["max_seqlen_k"])
+
 
 @dataclasses.dataclass
 class AttnCall:
@@ -47,6 +57,10 @@ class AttnCall:
     dropout_p: float = 0.0
     is_causal: bool = False
     varlen: Optional[VarlenPacking] = None
+    # sequence-parallel degrees (spec.py:99-100): a dense backend computes the
+    # attention of the heads and keys it is handed whatever they are
+    ulysses_world_size: int = 1
+    ring_world_size: int = 1
     attention_kwargs: dict = dataclasses.field(default_factory=dict)
 
 
@@ -65,7 +79,7 @@ def unmet(query, key, value, call) -> Optional[str]:
         return f"supports head dimension 64, 128 only, got {query.shape[-1]}"
     if query.shape[1] != key.shape[1] or key.shape[1] != value.shape[1]:
         return "supports MHA only (equal query and key/value head counts)"
-    if call is not None and call.attention_kwargs.get("attn_mask") is not None:
+    if call is not None and (getattr(call, "attention_kwargs", None) or {}).get("attn_mask") is not None:
         return "does not support attn_mask"
     return None
 

@@ -433,6 +433,23 @@ def _slot_rope(freqs_cos, freqs_sin, device, B, S, dh):
     return rope
 
 
+def _slot_norm(norm, D, query):
+    """(fp32 weight [D], eps) of a norm_q / norm_k argument: an RMSNorm module
+    (torch.nn.RMSNorm or diffusers' RMSNorm: its `weight`, None without an
+    elementwise affine, and its `eps`, which torch.nn.RMSNorm leaves None for
+    the input dtype's machine epsilon) or a bare weight tensor (eps 1e-6, the
+    Wan attention's norm eps)."""
+    if isinstance(norm, torch.Tensor):
+        w, eps = norm, 1e-6
+    else:
+        w, eps = getattr(norm, "weight", None), getattr(norm, "eps", 1e-6)
+        if eps is None:
+            eps = torch.finfo(query.dtype).eps
+    if w is None:
+        w = torch.ones(D, device=query.device)
+    return w.float().contiguous(), float(eps)
+
+
 def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
     """Drop-in for the reference's `fused_qk_norm_rope` slot
     (transformer_wan.py:24-25,111-115): query/key [B, S, D] bf16, norm_q/norm_k
@@ -447,8 +464,10 @@ def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
     packet pass the same tables), so a steady call allocates only the two outputs."""
     B, S, D = query.shape
     dh = D // heads
-    wq = getattr(norm_q, "weight", norm_q).float().contiguous()
-    wk = getattr(norm_k, "weight", norm_k).float().contiguous()
+    wq, eps_q = _slot_norm(norm_q, D, query)
+    wk, eps_k = _slot_norm(norm_k, D, query)
+    if eps_q != eps_k:
+        raise ValueError(f"norm_q and norm_k must share eps (got {eps_q} and {eps_k})")
     rope = _slot_rope(freqs_cos, freqs_sin, query.device, B, S, dh)
     qi, ki = query.reshape(B * S, D), key.reshape(B * S, D)
     if qi.dtype != _BF16 or qi.stride(1) != 1:
@@ -457,7 +476,7 @@ def fused_qk_norm_rope(query, key, norm_q, norm_k, freqs_cos, freqs_sin, heads):
         ki = ki.to(_BF16).contiguous()
     q = torch.empty((B * S, D), dtype=_BF16, device=query.device)
     k = torch.empty((B * S, D), dtype=_BF16, device=query.device)
-    ops.qk_norm_rope_(qi, ki, wq, wk, dh, 1e-6, rope=rope, out=(q, k))
+    ops.qk_norm_rope_(qi, ki, wq, wk, dh, eps_q, rope=rope, out=(q, k))
     return q.reshape(B, S, heads, dh), k.reshape(B, S, heads, dh)
 
 
@@ -472,5 +491,3 @@ def step_flops(cfg, tokens_per_request, text_len=512):
         total += per_block * cfg.layers
     return total
 
-
-_ = math

@@ -153,6 +153,33 @@ def test_fused_qk_norm_rope_slot():
     assert torch.equal(qd.cpu(), q.to(torch.bfloat16)) and torch.equal(kd.cpu(), k.to(torch.bfloat16))
 
 
+def test_fused_qk_norm_rope_slot_norm_modules():
+    """norm_q / norm_k passed as torch.nn.RMSNorm modules, as the reference's
+    processor passes attn.norm_q / attn.norm_k: their weights and eps (here 1e-5)
+    are the ones applied."""
+    wan = _wan()
+    B, S, D, H = 1, 300, 1536, 12
+    grid = (3, 10, 10)
+    q, k = bf(randn((B, S, D), 38)) * 1e-3, bf(randn((B, S, D), 39)) * 1e-3
+    q, k = bf(q), bf(k)
+    wq, wk = bf(randn((D,), 40, 0.1) + 1), bf(randn((D,), 41, 0.1) + 1)
+    mods = []
+    for w in (wq, wk):
+        m = torch.nn.RMSNorm(D, eps=1e-5).to(DEV)
+        with torch.no_grad():
+            m.weight.copy_(w)
+        mods.append(m)
+    cos, sin = ow.rope_freqs(grid)
+    oq, okk = wan.fused_qk_norm_rope(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16), *mods,
+                                     cos.reshape(1, S, 1, 128).to(DEV), sin.reshape(1, S, 1, 128).to(DEV), H)
+    rq, rk = ow.qk_norm_rope(q[0], k[0], wq, wk, cos, sin, H, eps=1e-5)
+    assert_close(oq[0].float().cpu(), rq, 0.99999, 5e-3, "slot q, module norms")
+    assert_close(okk[0].float().cpu(), rk, 0.99999, 5e-3, "slot k, module norms")
+    # rows of mean square ~1e-6 tell eps 1e-5 from 1e-6: the oracle at 1e-6 is far off
+    wrong, _ = ow.qk_norm_rope(q[0], k[0], wq, wk, cos, sin, H, eps=1e-6)
+    assert (oq[0].float().cpu() - wrong).norm() > 0.1 * wrong.norm()
+
+
 def test_fused_qk_norm_rope_slot_fresh_tables_of_equal_length():
     """Two packets of equal S but different grids, (2, 6, 25) then (2, 10, 15): the
     first packet's tables are freed before the second packet builds its own (as the

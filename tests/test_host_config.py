@@ -75,6 +75,28 @@ def test_slot_rope_cache_is_keyed_on_the_table_tensors(monkeypatch):
     assert wan._slot_rope(c2, s1, "cpu", 2, S, dh) is not r3        # other batch size: rebuilt
 
 
+def test_slot_norm_arguments():
+    """The slot's norm_q / norm_k may be RMSNorm modules (their weight and eps, the
+    input dtype's epsilon when torch.nn.RMSNorm's eps is None, unit weights without
+    an elementwise affine) or bare weight tensors (eps 1e-6)."""
+    import torch
+
+    from ditserve_amd import wan
+
+    q = torch.zeros(2, 3, 8, dtype=torch.bfloat16)
+    m = torch.nn.RMSNorm(8, eps=1e-5)
+    with torch.no_grad():
+        m.weight.copy_(torch.arange(8.0))
+    w, eps = wan._slot_norm(m, 8, q)
+    assert torch.equal(w, torch.arange(8.0)) and eps == 1e-5
+    w, eps = wan._slot_norm(torch.nn.RMSNorm(8), 8, q)
+    assert eps == torch.finfo(torch.bfloat16).eps
+    w, eps = wan._slot_norm(torch.nn.RMSNorm(8, eps=1e-6, elementwise_affine=False), 8, q)
+    assert torch.equal(w, torch.ones(8)) and eps == 1e-6
+    w, eps = wan._slot_norm(torch.full((8,), 2.0, dtype=torch.bfloat16), 8, q)
+    assert w.dtype == torch.float32 and torch.equal(w, torch.full((8,), 2.0)) and eps == 1e-6
+
+
 def test_view_extent_and_overlap():
     """linear_pair's aliasing check: byte ranges of strided views."""
     import torch
@@ -110,3 +132,23 @@ def test_model_inputs_refused_before_any_launch():
     for lat, txt in (((16, 800, 64), (10, 4096)), ((16, 64, 64), (10, 2048)), ((4, 64, 64), (10, 4096))):
         with pytest.raises(ValueError):
             s.forward_packed([torch.zeros(lat)], [1.0], [torch.zeros(txt)], [torch.zeros(2048)])
+
+
+def test_attention_plugin_dataclasses_match_reference():
+    """The plugin's call objects carry the reference's fields
+    (workers/xfuser/core/attention/spec.py:63-102), so a caller that builds them
+    by keyword builds ours the same way."""
+    import dataclasses
+
+    from ditserve_amd import attention
+
+    assert [f.name for f in dataclasses.fields(attention.VarlenPacking)] == [
+        "indices_k", "cu_seqlens_k", "max_seqlen_k"]
+    assert [f.name for f in dataclasses.fields(attention.AttnCall)] == [
+        "dropout_p", "is_causal", "varlen", "ulysses_world_size", "ring_world_size", "attention_kwargs"]
+    call = attention.AttnCall(ulysses_world_size=2, ring_world_size=2, attention_kwargs={"attn_mask": 1})
+    assert call.attention_kwargs["attn_mask"] == 1
+    assert attention.VarlenPacking.from_kwargs(None) is None
+    assert attention.VarlenPacking.from_kwargs({"cu_seqlens_k": 1}) is None
+    p = attention.VarlenPacking.from_kwargs({"indices_k": "i", "cu_seqlens_k": "c", "max_seqlen_k": 7})
+    assert (p.indices_k, p.cu_seqlens_k, p.max_seqlen_k) == ("i", "c", 7)

@@ -6,6 +6,10 @@ block, the Wan packet prelude/epilogue, and the SD3.5 packed MMDiT joint block.
 Each function cites the reference file:line it follows (paths relative to the
 reference repository root).
 
+The functions run wherever their inputs live: on the CPU as the restatement
+proper, and (a GPU test's full-size check only) on a GPU device in fp32, where the
+same torch operations compute the same formulas.
+
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker or the timed CPU
 baseline.  The product (``ditserve_amd``) never imports it: the GPU path fails

@@ -1,7 +1,7 @@
 """Oracle: shared elementwise / normalisation / attention pieces (CPU, fp32 or fp64).
 
 Every function computes in the dtype of its input (callers pass fp32 for the
-oracle proper and fp64 for pinning tests).
+oracle proper and fp64 for pinning tests) and on its input's device.
 """
 import math
 
@@ -60,7 +60,9 @@ def timestep_embedding(t, dim=256, flip_sin_to_cos=True, downscale_freq_shift=0.
     Used by the Wan condition embedder (transformer_wan.py:331-333 -> condition_embedder)
     and the SD3.5 time_text_embed (sd35_batch.py:642-644).  Returns [N, dim] fp32.
     """
-    t = torch.as_tensor(t, dtype=torch.float32).reshape(-1)
+    t = torch.as_tensor(t, dtype=torch.float32)
+    device = t.device                 # computed on the CPU, returned on t's device
+    t = t.cpu().reshape(-1)
     half = dim // 2
     exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32) / (half - downscale_freq_shift)
     freqs = torch.exp(exponent)
@@ -68,7 +70,7 @@ def timestep_embedding(t, dim=256, flip_sin_to_cos=True, downscale_freq_shift=0.
     emb = torch.cat([torch.sin(args), torch.cos(args)], dim=-1)
     if flip_sin_to_cos:
         emb = torch.cat([emb[:, half:], emb[:, :half]], dim=-1)
-    return emb
+    return emb.to(device)
 
 
 def sdpa(q, k, v, chunk=4096):
@@ -80,7 +82,7 @@ def sdpa(q, k, v, chunk=4096):
     processed in chunks so S x S scores are never materialised whole.
     """
     scale = 1.0 / math.sqrt(q.shape[-1])
-    out = torch.empty(q.shape[:-1] + (v.shape[-1],), dtype=q.dtype)
+    out = torch.empty(q.shape[:-1] + (v.shape[-1],), dtype=q.dtype, device=q.device)
     for s0 in range(0, q.shape[-2], chunk):
         qs = q[..., s0:s0 + chunk, :]
         scores = (qs @ k.transpose(-1, -2)) * scale
@@ -96,8 +98,9 @@ def sdpa_lse(q, k, v):
 
 
 def sdpa_fast(q, k, v):
-    """CPU flash SDPA (torch's fused CPU kernel; no S x S materialisation) — used for the
-    full-shape CPU baseline, where the chunked math path would be too slow."""
+    """Fused SDPA (torch's flash kernel on the CPU, its fp32 memory-efficient kernel on
+    a GPU; no S x S materialisation) — used at full shapes (the CPU baseline, the
+    full-size checks), where the chunked math path would be too slow."""
     return F.scaled_dot_product_attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)).squeeze(0)
 
 
@@ -109,7 +112,7 @@ def varlen_attention(q, k, v, cu_q, cu_k, attn=sdpa):
     (sd35_batch.py:19-119,448-486) and of its per-segment fake
     (tests/python/test_domain_block_executor.py:869-883).
     """
-    out = torch.empty(q.shape[:-1] + (v.shape[-1],), dtype=q.dtype)
+    out = torch.empty(q.shape[:-1] + (v.shape[-1],), dtype=q.dtype, device=q.device)
     for m in range(len(cu_q) - 1):
         q0, q1, k0, k1 = cu_q[m], cu_q[m + 1], cu_k[m], cu_k[m + 1]
         if q1 == q0:

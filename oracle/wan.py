@@ -228,9 +228,10 @@ def forward(p, cfg, latent, t, text, attn=sdpa, blocks=None):
     scalar timestep t, text [512, text_dim]. Returns the velocity prediction [C, F, H, W]."""
     pt, ph, pw = cfg["patch"]
     grid = (latent.shape[1] // pt, latent.shape[2] // ph, latent.shape[3] // pw)
-    cos, sin = rope_freqs(grid, cfg["head_dim"], cfg.get("rope_max_seq_len", 1024))
+    cos, sin = (x.to(latent.device) for x in rope_freqs(grid, cfg["head_dim"], cfg.get("rope_max_seq_len", 1024)))
     hidden = patch_embed(p, latent, cfg["patch"])
-    temb, projected, enc = condition_embedder(p, torch.tensor([float(t)]), text, cfg["freq_dim"])
+    temb, projected, enc = condition_embedder(p, torch.tensor([float(t)], device=latent.device), text,
+                                              cfg["freq_dim"])
     n_blocks = cfg["layers"] if blocks is None else blocks
     for i in range(n_blocks):
         hidden = block_forward(p, i, hidden, enc, projected[0], cos, sin, cfg["heads"], cfg["eps"], attn)

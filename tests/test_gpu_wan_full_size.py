@@ -10,6 +10,9 @@
   75600 tokens, a 4.6 GB fused QKV buffer), packed bitwise equal to solo; that
   pair's self-attention with q rows past 4 GiB of offsets, on sampled rows against
   an fp32 reference.
+* The full Wan2.1-1.3B 480x832x81 CFG-pair step (30 blocks, 2 x 32760 tokens)
+  against the oracle run in fp32 on the GPU: cos >= 0.999 and relative L2 <= 2e-2
+  per prediction.
 * One Wan2.2-5B block at 4096 tokens, one Wan2.1-14B block at 128 tokens and one
   Wan2.1 block at the full 21x30x52 grid (32760 tokens) against the CPU fp32
   oracle (torch's CPU flash SDPA for the 32760-token self-attention), cos >= 0.999
@@ -65,6 +68,39 @@ def test_wan21_30_blocks_480p_cfg_pair_bitwise():
         assert out.shape == (16, 21, 60, 104) and bool(torch.isfinite(out).all())
         assert torch.equal(out, model.forward_packed([lat], [999.0], [txt])[0])
     assert not torch.equal(both[0], both[1])
+
+
+def test_wan21_480p_full_step_matches_oracle():
+    """The headline step at its full size against the oracle: Wan2.1-1.3B
+    architecture, 30 blocks, latent 16x21x60x104 (480x832x81 frames), the CFG pair
+    packed as 2 x 32760 tokens (text valid 120 / 0, t = 999).  The oracle runs in
+    fp32 on the GPU, its attention through torch's fp32 memory-efficient SDPA
+    (checked first against a float64 softmax on sampled rows at this shape).  Each
+    prediction: cosine >= 0.999 and relative L2 <= 2e-2 over the whole step."""
+    from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer, random_state_dict
+    cfg, S = WAN21_T2V_1_3B, 32760
+    g = torch.Generator(device=DEV).manual_seed(12)
+    q, k, v = (torch.randn((cfg.heads, S, cfg.head_dim), generator=g, device=DEV) for _ in range(3))
+    rows = torch.arange(0, S, 4095, device=DEV)
+    ref = torch.softmax(q[:, rows].double() @ k.double().transpose(1, 2) / math.sqrt(cfg.head_dim), -1) @ v.double()
+    err = ((oc.sdpa_fast(q, k, v)[:, rows].double() - ref).norm() / ref.norm()).item()
+    assert err < 1e-5, f"fp32 SDPA relative error {err}"
+    del q, k, v, ref
+    sd = random_state_dict(cfg, seed=13, device=DEV)
+    model = WanTransformer(cfg, sd, DEV)
+    lat = randn((16, 21, 60, 104), 56).to(DEV)
+    texts = (_text(57, 120).to(DEV), torch.zeros(512, 4096, device=DEV))
+    got = [o.float().cpu() for o in model.forward_packed([lat, lat], [999.0, 999.0], list(texts))]
+    del model
+    torch.cuda.empty_cache()
+    ocfg = dict(patch=cfg.patch, head_dim=cfg.head_dim, heads=cfg.heads, layers=cfg.layers, freq_dim=cfg.freq_dim,
+                eps=cfg.eps, out_ch=cfg.out_ch)
+    with torch.no_grad():
+        for out, txt, label in zip(got, texts, ("cond", "uncond")):
+            ref = ow.forward(sd, ocfg, lat.bfloat16().float(), 999.0, txt.bfloat16().float(), attn=oc.sdpa_fast)
+            c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"wan2.1 480p 30-block step ({label})")
+            print(f"{label}: cos {c:.6f} relL2 {r:.3e}")
+            del ref
 
 
 def test_wan21_14b_two_blocks_720p_cfg_pair_bitwise():

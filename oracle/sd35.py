@@ -53,7 +53,8 @@ def patch_embed(p, latent, table, patch=2):
     c, h, w = latent.shape
     x = latent.reshape(c, h // patch, patch, w // patch, patch).permute(1, 3, 0, 2, 4).reshape(-1, c * patch * patch)
     wgt = p["pos_embed.proj.weight"].reshape(p["pos_embed.proj.weight"].shape[0], -1)
-    return linear(x, wgt, p["pos_embed.proj.bias"]) + cropped_pos_embed(table, h // patch, w // patch).to(x.dtype)
+    pos = cropped_pos_embed(table, h // patch, w // patch).to(device=x.device, dtype=x.dtype)
+    return linear(x, wgt, p["pos_embed.proj.bias"]) + pos
 
 
 def time_text_embed(p, t, pooled):
@@ -156,7 +157,7 @@ def forward(p, cfg, latent, t, text, pooled, attn=sdpa, table=None):
     table = pos_embed_table(cfg["dim"], cfg["pos_max"], cfg["base_size"]) if table is None else table
     h = patch_embed(p, latent, table, cfg["patch"])
     c = linear(text, p["context_embedder.weight"], p["context_embedder.bias"])
-    temb = time_text_embed(p, torch.tensor([float(t)]), pooled.reshape(1, -1))[0]
+    temb = time_text_embed(p, torch.tensor([float(t)], device=latent.device), pooled.reshape(1, -1))[0]
     for i in range(cfg["layers"]):
         h, c = joint_block(p, i, h, c, temb, cfg, attn)
     x = adaln_continuous(p, "norm_out", h, temb, cfg["eps"])

@@ -76,6 +76,32 @@ def test_sd35_medium_24_blocks_512px_matches_oracle():
     assert_close(out[0].cpu(), ref, 0.999, 2e-2, "sd35-medium 24 blocks")
 
 
+def test_sd35_medium_1024_cfg_pair_full_step_matches_oracle():
+    """The SD3.5-Medium 1024^2 CFG pair at full size (24 joint blocks, 13 dual; 2 x
+    (4096 image + 333 text) joint tokens, packed) against the oracle run in fp32 on
+    the GPU (torch's fp32 memory-efficient SDPA for its attention): each
+    prediction within cos >= 0.999 and relative L2 <= 2e-2."""
+    from oracle import common as oc
+    sd35 = _sd()
+    cfg = sd35.SD35_MEDIUM
+    sd = sd35.random_state_dict(cfg, seed=4, device=DEV)
+    model = sd35.SD35Transformer(cfg, sd, DEV)
+    (lat, txt_c, pool_c), (_, txt_u, pool_u) = _inputs(30, 1024), _inputs(33, 1024)
+    reqs = [(txt_u, pool_u), (txt_c, pool_c)]
+    outs, meta = model.forward_packed([lat.to(DEV)] * 2, [900.0] * 2, [t.to(DEV) for t, _ in reqs],
+                                      [p.to(DEV) for _, p in reqs])
+    assert meta["cu_seqlens_joint"] == [0, 4429, 8858]
+    outs = [o.cpu() for o in outs]
+    del model
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        for out, (txt, pooled), label in zip(outs, reqs, ("uncond", "cond")):
+            ref = osd.forward(sd, cfg.oracle_dict(), bf(lat).to(DEV), 900.0, bf(txt).to(DEV), bf(pooled).to(DEV),
+                              attn=oc.sdpa_fast)
+            c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"sd35-medium 1024 step ({label})")
+            print(f"{label}: cos {c:.6f} relL2 {r:.3e}")
+
+
 def test_sd35_config3_packed_cfg_batch_bitwise():
     """2 x 1024^2 + 4 x 512^2 requests, each as an (uncond, cond) CFG pair -> 12 packed
     segments; every segment equals its solo forward bitwise."""
@@ -108,6 +134,36 @@ def test_sd35_config3_packed_cfg_batch_bitwise():
                                            [pools[i]])
         assert torch.isfinite(solo[0]).all()
         assert torch.equal(outs[i], solo[0]), f"segment {i} differs"
+
+
+def test_sd35_config3_packed_cfg_batch_matches_oracle():
+    """The packed 2 x 1024^2 + 4 x 512^2 CFG batch (12 joint segments, 24 blocks) at
+    full size: every segment's prediction against the oracle run in fp32 on the GPU,
+    cos >= 0.999 and relative L2 <= 2e-2."""
+    from oracle import common as oc
+    sd35 = _sd()
+    cfg = sd35.SD35_MEDIUM
+    sd = sd35.random_state_dict(cfg, seed=5, device=DEV)
+    model = sd35.SD35Transformer(cfg, sd, DEV)
+    res = [1024, 1024, 512, 512, 512, 512]
+    segs = []
+    for r, size in enumerate(res):
+        lat, txt_c, pool_c = _inputs(40 + 3 * r, size)
+        txt_u, pool_u = torch.zeros_like(txt_c), torch.zeros_like(pool_c)
+        for txt, pool in ((txt_u, pool_u), (txt_c, pool_c)):
+            segs.append((lat, float(75 * (r + 1)), txt, pool))
+    outs, meta = model.forward_packed([x[0].to(DEV) for x in segs], [x[1] for x in segs],
+                                      [x[2].to(DEV) for x in segs], [x[3].to(DEV) for x in segs])
+    assert len(meta["cu_seqlens_joint"]) == 13
+    outs = [o.cpu() for o in outs]
+    del model
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        for i, ((lat, t, txt, pool), out) in enumerate(zip(segs, outs)):
+            ref = osd.forward(sd, cfg.oracle_dict(), bf(lat).to(DEV), t, bf(txt).to(DEV), bf(pool).to(DEV),
+                              attn=oc.sdpa_fast)
+            c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"segment {i} ({res[i // 2]}^2, t={t})")
+            print(f"segment {i} ({res[i // 2]}^2): cos {c:.6f} relL2 {r:.3e}")
 
 
 REFERENCE_BATCH = {"results", "batch_size", "quantum", "model_ms", "attention", "bubble_free", "sequence_packing",

@@ -10,9 +10,10 @@
   75600 tokens, a 4.6 GB fused QKV buffer), packed bitwise equal to solo; that
   pair's self-attention with q rows past 4 GiB of offsets, on sampled rows against
   an fp32 reference.
-* The full Wan2.1-1.3B 480x832x81 CFG-pair step (30 blocks, 2 x 32760 tokens)
-  against the oracle run in fp32 on the GPU: cos >= 0.999 and relative L2 <= 2e-2
-  per prediction.
+* The full Wan2.1-1.3B 480x832x81 and Wan2.2-5B 704x1280x121 CFG-pair steps (30
+  blocks, 2 x 32760 and 2 x 27280 tokens) and the 4-request packed batch (56400
+  tokens) against the oracle run in fp32 on the GPU: cos >= 0.999 and relative L2
+  <= 2e-2 per prediction.
 * One Wan2.2-5B block at 4096 tokens, one Wan2.1-14B block at 128 tokens and one
   Wan2.1 block at the full 21x30x52 grid (32760 tokens) against the CPU fp32
   oracle (torch's CPU flash SDPA for the 32760-token self-attention), cos >= 0.999
@@ -100,6 +101,60 @@ def test_wan21_480p_full_step_matches_oracle():
             ref = ow.forward(sd, ocfg, lat.bfloat16().float(), 999.0, txt.bfloat16().float(), attn=oc.sdpa_fast)
             c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"wan2.1 480p 30-block step ({label})")
             print(f"{label}: cos {c:.6f} relL2 {r:.3e}")
+            del ref
+
+
+def test_wan22_5b_full_step_matches_oracle():
+    """The Wan2.2-TI2V-5B step at its full size (30 blocks, latent 48x31x44x80 for
+    704x1280x121 frames, the CFG pair packed as 2 x 27280 tokens, text valid 150 /
+    0, t = 700) against the oracle run in fp32 on the GPU: each prediction within
+    cos >= 0.999 and relative L2 <= 2e-2."""
+    from ditserve_amd.wan import WAN22_TI2V_5B, WanTransformer, random_state_dict
+    cfg = WAN22_TI2V_5B
+    sd = random_state_dict(cfg, seed=14, device=DEV)
+    model = WanTransformer(cfg, sd, DEV)
+    lat = randn((48, 31, 44, 80), 58).to(DEV)
+    texts = (_text(59, 150).to(DEV), torch.zeros(512, 4096, device=DEV))
+    got = [o.float().cpu() for o in model.forward_packed([lat, lat], [700.0, 700.0], list(texts))]
+    del model
+    torch.cuda.empty_cache()
+    ocfg = dict(patch=cfg.patch, head_dim=cfg.head_dim, heads=cfg.heads, layers=cfg.layers, freq_dim=cfg.freq_dim,
+                eps=cfg.eps, out_ch=cfg.out_ch)
+    with torch.no_grad():
+        for out, txt, label in zip(got, texts, ("cond", "uncond")):
+            ref = ow.forward(sd, ocfg, lat.bfloat16().float(), 700.0, txt.bfloat16().float(), attn=oc.sdpa_fast)
+            c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"wan2.2-5b 704p 30-block step ({label})")
+            print(f"{label}: cos {c:.6f} relL2 {r:.3e}")
+            del ref
+
+
+def test_wan_packed_batch_config2_full_size_matches_oracle():
+    """The 4-request packed batch at full size (latents 21x60x104, 9x60x104, 13x40x64
+    and 5x32x32: 32760 + 14040 + 8320 + 1280 = 56400 tokens; timesteps drawn in
+    [0, 1000), texts with 30-200 valid rows), 30 blocks: each request's packed
+    prediction against the oracle run in fp32 on the GPU, cos >= 0.999 and relative
+    L2 <= 2e-2."""
+    from ditserve_amd.wan import WAN21_T2V_1_3B, WanTransformer, random_state_dict
+    cfg = WAN21_T2V_1_3B
+    sd = random_state_dict(cfg, seed=15, device=DEV)
+    model = WanTransformer(cfg, sd, DEV)
+    g = torch.Generator().manual_seed(16)
+    shapes = [(16, 21, 60, 104), (16, 9, 60, 104), (16, 13, 40, 64), (16, 5, 32, 32)]
+    lats = [torch.randn(s, generator=g).to(DEV) for s in shapes]
+    ts = [float(x) for x in (torch.rand(4, generator=g) * 1000)]
+    valid = [int(x) for x in torch.randint(30, 201, (4,), generator=g)]
+    texts = [_text(60 + i, valid[i]).to(DEV) for i in range(4)]
+    got = [o.float().cpu() for o in model.forward_packed(lats, ts, texts)]
+    del model
+    torch.cuda.empty_cache()
+    ocfg = dict(patch=cfg.patch, head_dim=cfg.head_dim, heads=cfg.heads, layers=cfg.layers, freq_dim=cfg.freq_dim,
+                eps=cfg.eps, out_ch=cfg.out_ch)
+    with torch.no_grad():
+        for i, out in enumerate(got):
+            ref = ow.forward(sd, ocfg, lats[i].bfloat16().float(), ts[i], texts[i].bfloat16().float(),
+                             attn=oc.sdpa_fast)
+            c, r = assert_close(out, ref.cpu(), 0.999, 2e-2, f"packed request {i} {shapes[i]} t={ts[i]:.1f}")
+            print(f"request {i} {shapes[i]}: cos {c:.6f} relL2 {r:.3e}")
             del ref
 
 

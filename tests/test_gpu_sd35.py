@@ -48,6 +48,29 @@ def test_sd35_small_depth_packed_matches_oracle_and_solo():
         assert torch.equal(outs[m], solo[0]), f"request {m}: packed != solo"
 
 
+def test_sd35_non_square_packed_matches_oracle_and_solo():
+    """Non-square requests packed together: 1024 x 576 and 512 x 768 pixels (64 x 36 and
+    32 x 48 patches), 3 blocks (dual attention in block 0, context_pre_only block 2),
+    own timesteps: each against the oracle and bitwise equal to its solo run (the
+    position crop, patchify and unpatchify keep rows and columns apart)."""
+    sd35 = _sd()
+    cfg = sd35.SD35Config(layers=3, dual_layers=(0,))
+    sd = sd35.random_state_dict(cfg, seed=6)
+    model = sd35.SD35Transformer(cfg, sd, DEV)
+    lats = [randn((16, 128, 72), 70), randn((16, 64, 96), 71)]
+    txts, pools = [randn((333, 4096), 72), randn((333, 4096), 73)], [randn((2048,), 74), randn((2048,), 75)]
+    ts = [640.0, 120.0]
+    outs, meta = model.forward_packed([x.to(DEV) for x in lats], ts, [x.to(DEV) for x in txts],
+                                      [x.to(DEV) for x in pools])
+    assert meta["cu_seqlens_img"] == [0, 2304, 3840]
+    for m in range(2):
+        assert outs[m].shape == lats[m].shape
+        ref = osd.forward(sd, cfg.oracle_dict(), bf(lats[m]), ts[m], bf(txts[m]), bf(pools[m]))
+        assert_close(outs[m].cpu(), ref, 0.999, 2e-2, f"sd35 non-square request {m}")
+        solo, _ = model.forward_packed([lats[m].to(DEV)], [ts[m]], [txts[m].to(DEV)], [pools[m].to(DEV)])
+        assert torch.equal(outs[m], solo[0]), f"request {m}: packed != solo"
+
+
 def test_sd35_large_shaped_blocks_match_oracle():
     """The SD3.5-Large block shape (38 heads of 64, hidden 2432, FFN 9728, no dual
     attention, position table 192), two blocks (the second context_pre_only) at 256^2."""

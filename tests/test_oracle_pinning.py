@@ -238,6 +238,17 @@ def test_sd35_pos_embed_closed_form_and_crop():
     assert abs(float(c192[3 * 16 + 5, 2]) - math.sin((c * 64 / 192) * w)) < 1e-6
     assert abs(float(c192[3 * 16 + 5, 32 + 2]) - math.sin((r * 64 / 192) * w)) < 1e-6
     assert torch.allclose(pos_embed_crop(SD35Config(dim=64, pos_max=192), 16, 16, "cpu"), c192, atol=1e-6)
+    # a non-square grid (40 patch rows x 72 patch columns, e.g. 640 x 1152 pixels): rows crop
+    # from 172, columns from 156, tokens row-major; a transposed crop fails here
+    cn = osd.cropped_pos_embed(table, 40, 72)
+    assert cn.shape == (40 * 72, 64)
+    for i, j in ((0, 0), (3, 61), (39, 71)):
+        r, c = 172 + i, 156 + j
+        for k in (1, 9):
+            w = 1.0 / 10000 ** (k / 16.0)
+            assert abs(float(cn[i * 72 + j, k]) - math.sin((c * 64 / 384) * w)) < 1e-6
+            assert abs(float(cn[i * 72 + j, 32 + 16 + k]) - math.cos((r * 64 / 384) * w)) < 1e-6
+    assert torch.allclose(pos_embed_crop(SD35Config(dim=64), 40, 72, "cpu"), cn, atol=1e-6)
 
 
 def test_sd35_adaln_chunk_orders():

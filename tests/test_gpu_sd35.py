@@ -51,18 +51,20 @@ def test_sd35_small_depth_packed_matches_oracle_and_solo():
 def test_sd35_non_square_packed_matches_oracle_and_solo():
     """Non-square requests packed together: 1024 x 576 and 512 x 768 pixels (64 x 36 and
     32 x 48 patches), 3 blocks (dual attention in block 0, context_pre_only block 2),
-    own timesteps: each against the oracle and bitwise equal to its solo run (the
-    position crop, patchify and unpatchify keep rows and columns apart)."""
+    own timesteps and prompt lengths (333 and 154 text tokens): each against the oracle
+    and bitwise equal to its solo run (the position crop, patchify and unpatchify keep
+    rows and columns apart; the joint seams sit at different offsets)."""
     sd35 = _sd()
     cfg = sd35.SD35Config(layers=3, dual_layers=(0,))
     sd = sd35.random_state_dict(cfg, seed=6)
     model = sd35.SD35Transformer(cfg, sd, DEV)
     lats = [randn((16, 128, 72), 70), randn((16, 64, 96), 71)]
-    txts, pools = [randn((333, 4096), 72), randn((333, 4096), 73)], [randn((2048,), 74), randn((2048,), 75)]
+    txts, pools = [randn((333, 4096), 72), randn((154, 4096), 73)], [randn((2048,), 74), randn((2048,), 75)]
     ts = [640.0, 120.0]
     outs, meta = model.forward_packed([x.to(DEV) for x in lats], ts, [x.to(DEV) for x in txts],
                                       [x.to(DEV) for x in pools])
-    assert meta["cu_seqlens_img"] == [0, 2304, 3840]
+    assert meta["cu_seqlens_img"] == [0, 2304, 3840] and meta["cu_seqlens_txt"] == [0, 333, 487]
+    assert meta["cu_seqlens_joint"] == [0, 2637, 4327]
     for m in range(2):
         assert outs[m].shape == lats[m].shape
         ref = osd.forward(sd, cfg.oracle_dict(), bf(lats[m]), ts[m], bf(txts[m]), bf(pools[m]))

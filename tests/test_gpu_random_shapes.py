@@ -7,6 +7,7 @@ oracle's formulas evaluated in fp32 on the GPU (the same bf16-rounded inputs).
 * Varlen attention: 1-5 segments of 0-900 queries and 0-900 keys (segments without
   queries or without keys included), 1-4 heads of 64 or 128, plain and pre-scaled q.
   Rows of a segment without keys are zero.  cos >= 0.9999, relative L2 <= 1e-2.
+* Joint attention from two sources: 1-4 segments of 0-700 image and 0-400 text rows.
 * AdaLN (LayerNorm / RMSNorm, modulated over random segments or affine) and per-head
   or across-head QK RMSNorm at random T and D <= 6144.
 The shapes are drawn once from a fixed seed (segment cuts per case from its own
@@ -136,6 +137,51 @@ def test_attention_random_segment_tables(lq, lk, heads, hd, pre):
     cos, rel = _metrics(out, ref)
     print(f"attention q{lq} k{lk} heads {heads} hd {hd} pre={pre}: cos {cos:.6f} rel {rel:.2e}")
     assert torch.isfinite(out).all() and cos >= 0.9999 and rel <= 1e-2
+
+
+JOINT_RANDOM = []
+for _ in range(10):
+    nseg = RNG.randint(1, 4)
+    li = [RNG.randint(1, 700) if RNG.random() < 0.8 else 0 for _ in range(nseg)]
+    lt = [RNG.randint(1, 400) if RNG.random() < 0.8 else 0 for _ in range(nseg)]
+    li[0], lt[-1] = li[0] or RNG.randint(1, 700), lt[-1] or RNG.randint(1, 400)  # both sources non-empty
+    JOINT_RANDOM.append((tuple(li), tuple(lt), RNG.randint(1, 4)))
+
+
+@pytest.mark.parametrize("li,lt,heads", JOINT_RANDOM)
+def test_joint_attention_random_layouts(li, lt, heads):
+    """Joint attention read in place from the image and text projections (head_dim 64,
+    q pre-scaled): segment m attends over its image rows followed by its text rows; the
+    image/text seam falls at every offset the random lengths give."""
+    ops = _ops()
+    hd, W = 64, heads * 64
+    cu_i, cu_t = _cu(li), _cu(lt)
+    cu_j = [a + b for a, b in zip(cu_i, cu_t)]
+    seg_i, seg_t, seg_j = ops.Segments(cu_i, DEV), ops.Segments(cu_t, DEV), ops.Segments(cu_j, DEV)
+    g = _g(cu_i[-1] * 5 + cu_t[-1] * 3 + heads)
+    qkv_i = torch.randn((cu_i[-1], 3 * W), generator=g, device=DEV).bfloat16()
+    qkv_t = torch.randn((cu_t[-1], 3 * W), generator=g, device=DEV).bfloat16()
+    scale = ops.LOG2E / math.sqrt(hd)
+    qkv_i[:, :W] = (qkv_i[:, :W].float() * scale).bfloat16()
+    qkv_t[:, :W] = (qkv_t[:, :W].float() * scale).bfloat16()
+    vt = ops.transpose_v_joint(qkv_i[:, 2 * W:], qkv_t[:, 2 * W:], heads, hd, seg_i, seg_t, seg_j)
+    o_i, o_t = ops.joint_attention_q_prescaled(qkv_i[:, :W], qkv_t[:, :W], qkv_i[:, W:2 * W], qkv_t[:, W:2 * W],
+                                               vt, seg_i, seg_t, seg_j, heads, hd)
+    r_i, r_t = torch.zeros_like(o_i, dtype=torch.float32), torch.zeros_like(o_t, dtype=torch.float32)
+    for m in range(len(li)):
+        rows = torch.cat([qkv_i[cu_i[m]:cu_i[m + 1]], qkv_t[cu_t[m]:cu_t[m + 1]]]).float()
+        if rows.shape[0] == 0:
+            continue
+        q = (rows[:, :W] / ops.LOG2E).view(-1, heads, hd).transpose(0, 1)
+        k = rows[:, W:2 * W].view(-1, heads, hd).transpose(0, 1)
+        v = rows[:, 2 * W:].view(-1, heads, hd).transpose(0, 1)
+        o = torch.matmul(torch.softmax(torch.matmul(q, k.transpose(1, 2).contiguous()), dim=-1), v)
+        o = o.transpose(0, 1).reshape(-1, W)
+        r_i[cu_i[m]:cu_i[m + 1]], r_t[cu_t[m]:cu_t[m + 1]] = o[:li[m]], o[li[m]:]
+    for got, ref, name in ((o_i, r_i, "image"), (o_t, r_t, "text")):
+        cos, rel = _metrics(got.float(), ref)
+        print(f"joint img{li} txt{lt} heads {heads} ({name} rows): cos {cos:.6f} rel {rel:.2e}")
+        assert torch.isfinite(got.float()).all() and cos >= 0.9999 and rel <= 1e-2
 
 
 ROW_RANDOM = []
